@@ -1,0 +1,150 @@
+/*
+ * camhip.h -- C ABI of the MI355X (gfx950) CAM MoE hot path.
+ *
+ * Drop-in for the aclnn two-phase interface of UMDK CAM
+ * (src/cam/comm_operator/ascend_kernels/<op>/op_api/aclnn_<op>.h):
+ *
+ *   status = camhipXxxGetWorkspaceSize(inputs..., attrs..., outputs...,
+ *                                      &workspaceSize, &executor);
+ *   status = camhipXxx(workspace, workspaceSize, executor, stream);
+ *
+ * Tensors are plain device pointers with explicit sizes; the caller owns
+ * every input, output and workspace buffer.  The executor is owned by the
+ * library and freed by the second call, whether it launches or fails.
+ * Launches are asynchronous and ordered on `stream` (a hipStream_t, NULL for
+ * the default stream).  No call synchronises with the host or allocates
+ * device memory.  Calls that share a workspace must not overlap.
+ *
+ * Every function returns CAMHIP_SUCCESS (0) or an error code; the message of
+ * the last error on the calling thread is camhipGetLastErrorMsg().
+ *
+ * Layouts: bf16 tensors are uint16 bit patterns, fp8 tensors are OCP e4m3fn
+ * byte codes, all row-major and contiguous unless stated.
+ *
+ * This build runs one EP rank on one GPU: epWorldSize/rankSize must be 1 for
+ * the dispatch, notify and combine calls (the reference requires 2..384 ranks,
+ * moe_dispatch_prefill.cpp:63, and exchanges rows between ranks).
+ */
+#ifndef CAMHIP_H
+#define CAMHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CAMHIP_API __attribute__((visibility("default")))
+
+typedef int camhipStatus;
+#define CAMHIP_SUCCESS 0
+#define CAMHIP_ERROR_INVALID_PARAM 161001 /* same code aclnn uses for ACLNN_ERR_PARAM_INVALID */
+#define CAMHIP_ERROR_NULLPTR 161002
+#define CAMHIP_ERROR_RUNTIME 361001       /* a HIP launch failed */
+#define CAMHIP_ERROR_WORKSPACE 161003     /* workspace smaller than requested */
+
+typedef struct camhipExecutor camhipExecutor;
+
+/* Quantisation of dispatched rows (quantMode attribute of aclnnMoeDispatchNormal). */
+#define CAMHIP_QUANT_NONE 0        /* bf16 rows, scales untouched */
+#define CAMHIP_QUANT_INT8_TOKEN 2  /* int8, one fp32 scale per row (reference use_quant=True) */
+#define CAMHIP_QUANT_FP8_BLOCK 3   /* fp8 e4m3fn, one fp32 scale per 1x128 block (extension) */
+
+CAMHIP_API const char *camhipGetLastErrorMsg(void);
+CAMHIP_API const char *camhipGetVersion(void);
+
+/* ------------------------------------------------------------------ routing
+ * No reference counterpart (CAM callers compute topk_idx themselves,
+ * src/cam/examples/moe_dispatch_combine_prefill_sample.py:87-93).
+ * logits [numTokens, numExperts] fp32, bias [numExperts] fp32 or NULL.
+ * topkIdx[t,k]: the k-th largest logit+bias (ties -> lower expert id).
+ * topkWeights[t,k] = softmax(logits[t])[topkIdx[t,k]] renormalised over the K picks.
+ * Limits: 1 <= topK <= 16, topK <= numExperts <= 512. */
+CAMHIP_API camhipStatus camhipMoeRouteGetWorkspaceSize(const float *logits, const float *bias, int64_t numTokens,
+                                                       int64_t numExperts, int64_t topK, int32_t *topkIdx,
+                                                       float *topkWeights, uint64_t *workspaceSize,
+                                                       camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoeRoute(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                       void *stream);
+
+/* ------------------------------------------------------------------ layout
+ * Replaces aclnnDispatchLayoutGetWorkspaceSize / aclnnDispatchLayout
+ * (dispatch_layout/op_api/aclnn_dispatch_layout.h:33-46; kernel
+ * dispatch_layout.h:83-166).  topkIdx [numTokens, numTopk] int64.
+ * Outputs: numTokensPerRank [numRanks] (may be NULL), numTokensPerExpert
+ * [numExperts], isTokenInRank [numTokens, numRanks] (may be NULL),
+ * sendTokenIdxSmall [numTokens, numTopk] = stable rank of (t,k) within its
+ * expert.  The reference's notifySendData scratch lives in the workspace.
+ * Expert ids outside [0,numExperts) are not routed (sendTokenIdx = -1).
+ * Limits (dispatch_layout_tiling.cpp:55-65,98-122): numRanks in [1,384],
+ * numExperts in [1,512] and divisible by numRanks, numTopk in [1,16],
+ * numTokens in [0,65536] (the reference stops at 8000). */
+CAMHIP_API camhipStatus camhipDispatchLayoutGetWorkspaceSize(const int64_t *topkIdx, int64_t numTokens,
+                                                             int64_t numRanks, int64_t numExperts, int64_t numTopk,
+                                                             int32_t *numTokensPerRank, int32_t *numTokensPerExpert,
+                                                             int32_t *isTokenInRank, int32_t *sendTokenIdxSmall,
+                                                             uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipDispatchLayout(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                             void *stream);
+
+/* ------------------------------------------------------------------ notify
+ * Replaces aclnnNotifyDispatch (notify_dispatch/op_api/aclnn_notify_dispatch.h:19-27;
+ * kernel notify_dispatch.h:129-160, 306-412) for a single rank.
+ * tokenPerExpertData [numExperts] int32 -> sendDataOffset [numExperts]
+ * (exclusive prefix), totalRecvTokens [1], recvCount [numExperts] (inclusive
+ * prefix, expert-major), recvOffset [numExperts], maxBs [1] = numTokens,
+ * recvTokensPerExpert [numExperts/rankSize] int64.  Optional outputs may be
+ * NULL except sendDataOffset. */
+CAMHIP_API camhipStatus camhipNotifyDispatchGetWorkspaceSize(const int32_t *tokenPerExpertData, int64_t numExperts,
+                                                             int64_t numTokens, int64_t rankSize, int64_t rankId,
+                                                             int32_t *sendDataOffset, int32_t *totalRecvTokens,
+                                                             int32_t *recvCount, int32_t *recvOffset, int32_t *maxBs,
+                                                             int64_t *recvTokensPerExpert, uint64_t *workspaceSize,
+                                                             camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipNotifyDispatch(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                             void *stream);
+
+/* ------------------------------------------------------------------ dispatch
+ * Replaces aclnnMoeDispatchNormal (moe_dispatch_normal/op_api/aclnn_moe_dispatch_normal.h:19-27;
+ * kernel moe_dispatch_normal.h:295-410, 545-591).
+ * x [numTokens, hidden] bf16, topkIdx/sendTokenIdx [numTokens, numTopk] int32,
+ * sendOffset [moeExpertNum].  recvOffset/recvCount are accepted for signature
+ * parity and unused with one rank (may be NULL).
+ * Output row of (t,k) = sendOffset[e] + sendTokenIdx[t,k]; rows must fit in
+ * recvRowsCapacity.  recvX [rows, hidden]: bf16 (quantMode 0), int8 (2) or
+ * fp8 e4m3fn (3).  recvXScales: untouched (0), [rows] (2), [rows, hidden/128] (3).
+ * assistInfoForCombine [rows, 3] int32 = (epRankId, t, k).
+ * Limits (moe_dispatch_normal_tiling.cpp:72-94): hidden in [1024,7168] and a
+ * multiple of 16 (of 128 for quantMode 3), numTopk in [1,16], moeExpertNum
+ * in [1,512], epWorldSize == 1. */
+CAMHIP_API camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(
+    const uint16_t *x, const int32_t *topkIdx, const int32_t *sendOffset, const int32_t *sendTokenIdx,
+    const int32_t *recvOffset, const int32_t *recvCount, int64_t numTokens, int64_t hidden, int64_t numTopk,
+    int64_t epWorldSize, int64_t epRankId, int64_t moeExpertNum, int64_t quantMode, int64_t recvRowsCapacity,
+    void *recvX, float *recvXScales, int32_t *assistInfoForCombine, uint64_t *workspaceSize,
+    camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoeDispatchNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                                void *stream);
+
+/* ------------------------------------------------------------------ combine
+ * Replaces aclnnMoeCombineNormal (moe_combine_normal/op_api/aclnn_moe_combine_normal.h:19-27;
+ * kernel moe_combine_normal.h:223-412).
+ * recvX [numRecvRows, hidden] bf16 expert outputs in dispatch order,
+ * tokenSrcInfo [numRecvRows, 3] = (rank, t, k) from dispatch, epRecvCounts
+ * [moeExpertNum] (its last entry bounds the rows used; may be NULL),
+ * recvTopkWeights [numTokens, numTopk] fp32 -> out [numTokens, hidden] bf16:
+ * out[t] = bf16_rne(sum_k float(row(t,k)) * w[t,k]), fp32, k ascending, no FMA.
+ * (t,k) slots that received no row contribute nothing.
+ * Limits: hidden in [1024,7168] and a multiple of 16, numTopk in [1,16],
+ * epWorldSize == 1. */
+CAMHIP_API camhipStatus camhipMoeCombineNormalGetWorkspaceSize(
+    const uint16_t *recvX, const int32_t *tokenSrcInfo, int64_t numRecvRows, const int32_t *epRecvCounts,
+    const float *recvTopkWeights, int64_t numTokens, int64_t numTopk, int64_t hidden, int64_t epWorldSize,
+    int64_t epRankId, int64_t moeExpertNum, uint16_t *out, uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                               void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CAMHIP_H */

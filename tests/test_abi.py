@@ -1,0 +1,105 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point that
+include/camhip.h declares, and rejects invalid arguments with the documented
+status codes and messages (the reference's tiling range checks,
+dispatch_layout_tiling.cpp:98-122, moe_dispatch_normal_tiling.cpp:72-94).
+No kernel is launched: only GetWorkspaceSize and the workspace check of the
+second phase run, which never touch a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "camhip.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from umdk_amd import _lib
+    return _lib.lib()
+
+
+def declared():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"CAMHIP_API\s+[^;(]*?\b(camhip\w+)\s*\(", txt)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "camhipDispatchLayoutGetWorkspaceSize" in names and "camhipMoeCombineNormal" in names
+    assert len(names) >= 12
+
+
+def test_library_exports_every_declared_symbol(L):
+    missing = [n for n in declared() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_two_phase_pair():
+    from umdk_amd import _lib
+    two_phase = {n[: -len("GetWorkspaceSize")] for n in declared() if n.endswith("GetWorkspaceSize")}
+    assert two_phase == set(_lib.SIGNATURES)
+
+
+def _ws(L, name, *args):
+    ws = ctypes.c_uint64(0)
+    ex = ctypes.c_void_p(0)
+    st = getattr(L, name + "GetWorkspaceSize")(*args, ctypes.byref(ws), ctypes.byref(ex))
+    return st, ws.value, ex, L.camhipGetLastErrorMsg().decode()
+
+
+P = 0x1000  # a non-NULL stand-in pointer: never dereferenced by the first phase
+
+
+@pytest.mark.parametrize("T,R,E,K,frag", [
+    (10, 0, 8, 2, "numRanks"), (10, 385, 768, 2, "numRanks"), (10, 1, 513, 2, "numExperts"),
+    (10, 3, 8, 2, "divisible"), (10, 1, 8, 17, "numTopk"), (10, 1, 8, 0, "numTopk"), (70000, 1, 8, 2, "numTokens"),
+])
+def test_layout_rejects_out_of_range(L, T, R, E, K, frag):
+    st, _, _, msg = _ws(L, "camhipDispatchLayout", P, T, R, E, K, P, P, P, P)
+    assert st == 161001 and frag in msg
+
+
+def test_layout_null_output_is_rejected(L):
+    st, _, _, msg = _ws(L, "camhipDispatchLayout", P, 10, 1, 8, 2, None, None, None, P)
+    assert st == 161002 and "numTokensPerExpert" in msg
+
+
+def test_layout_workspace_size_and_short_workspace(L):
+    st, ws, ex, _ = _ws(L, "camhipDispatchLayout", P, 4096, 1, 256, 8, P, P, P, P)
+    assert st == 0
+    assert ws == 4 * 32 * (256 + 1)   # 32 chunks of 1024 entries, E+R counters each
+    # second phase with a short workspace: rejected before any launch, executor freed
+    st2 = L.camhipDispatchLayout(None, 0, ex, None)
+    assert st2 == 161003 and "workspace" in L.camhipGetLastErrorMsg().decode()
+
+
+@pytest.mark.parametrize("H,q,frag", [(1000, 0, "hidden"), (8192, 0, "hidden"), (1040, 3, "128"), (1024, 1, "quantMode")])
+def test_dispatch_rejects_bad_hidden_and_quant(L, H, q, frag):
+    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, H, 2, 1, 0, 8, q, 8, P, P, P)
+    assert st == 161001 and frag in msg
+
+
+def test_dispatch_and_combine_need_single_rank(L):
+    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, 1024, 2, 2, 0, 8, 0, 8, P, P, P)
+    assert st == 161001 and "one EP rank" in msg
+    st, _, _, msg = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 2, 1, 8, P)
+    assert st == 161001 and "one EP rank" in msg
+    st, _, _, msg = _ws(L, "camhipNotifyDispatch", P, 8, 4, 2, 0, P, P, P, P, P, P)
+    assert st == 161001 and "one EP rank" in msg
+
+
+def test_route_limits(L):
+    st, _, _, msg = _ws(L, "camhipMoeRoute", P, None, 4, 8, 9, P, P)
+    assert st == 161001 and "topK" in msg
+    st, ws, ex, _ = _ws(L, "camhipMoeRoute", P, None, 4, 8, 2, P, P)
+    assert st == 0 and ws == 0
+    assert L.camhipMoeRoute(None, 0, None, None) == 161002  # NULL executor
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    import umdk_amd  # noqa: F401
+    with pytest.raises(Exception):
+        torch.ops.umdk_cam_op_lib.get_dispatch_layout(torch.zeros(4, 2, dtype=torch.int64), 8, 1)

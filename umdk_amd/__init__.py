@@ -1,0 +1,10 @@
+"""umdk_amd -- MI355X (gfx950) implementation of UMDK CAM's MoE hot path.
+
+Importing the package registers torch.ops.umdk_cam_op_lib.* (the reference's
+operator library name) and exposes the same module-level functions as the
+reference's pybind module (src/cam/comm_operator/pybind/pybind.cpp:13-19).
+"""
+from . import ops  # noqa: F401  (registers torch.ops.umdk_cam_op_lib)
+from .ops import get_dispatch_layout, moe_combine_prefill, moe_dispatch_prefill, moe_route  # noqa: F401
+
+__all__ = ["get_dispatch_layout", "moe_dispatch_prefill", "moe_combine_prefill", "moe_route"]

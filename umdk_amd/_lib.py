@@ -1,0 +1,90 @@
+"""Loader for libcamhip.so and a thin two-phase caller over its C ABI.
+
+The library must already be built (``python -m umdk_amd.build`` or
+``__graft_entry__.build()``); there is no fallback path: a missing library or
+a non-GPU tensor raises.
+"""
+import ctypes
+import os
+
+import torch  # loads the HIP runtime first, so libcamhip binds to the same one
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libcamhip.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+_U64P = ctypes.POINTER(ctypes.c_uint64)
+_EXP = ctypes.POINTER(ctypes.c_void_p)
+
+# argument kinds of each *GetWorkspaceSize entry point ('p' pointer, 'i' int64)
+SIGNATURES = {
+    "camhipMoeRoute": "pp iii pp",
+    "camhipDispatchLayout": "p iiii pppp",
+    "camhipNotifyDispatch": "p iiii pppppp",
+    "camhipMoeDispatchNormal": "pppppp iiiiiiii ppp",
+    "camhipMoeCombineNormal": "pp i pp iiiiii p",
+}
+
+_lib = None
+
+
+class CamHipError(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m umdk_amd.build` (there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.camhipGetLastErrorMsg.restype = ctypes.c_char_p
+        L.camhipGetVersion.restype = ctypes.c_char_p
+        for name, sig in SIGNATURES.items():
+            kinds = sig.replace(" ", "")
+            f = getattr(L, name + "GetWorkspaceSize")
+            f.restype = ctypes.c_int
+            f.argtypes = [(_P if k == "p" else _I) for k in kinds] + [_U64P, _EXP]
+            g = getattr(L, name)
+            g.restype = ctypes.c_int
+            g.argtypes = [_P, ctypes.c_uint64, _P, _P]
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return [n + s for n in SIGNATURES for s in ("GetWorkspaceSize", "")] + [
+        "camhipGetLastErrorMsg", "camhipGetVersion"]
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise CamHipError("umdk_cam_op_lib ops run on the GPU only; got a tensor on " + str(t.device))
+    if not t.is_contiguous():
+        raise CamHipError("umdk_cam_op_lib ops need contiguous tensors")
+    return t.data_ptr()
+
+
+def call(name, *args, device=None, stream=None):
+    """Runs one two-phase entry point: size the workspace, allocate it from
+    torch's caching allocator on `device`, launch on the current stream."""
+    L = lib()
+    ws = ctypes.c_uint64(0)
+    ex = ctypes.c_void_p(0)
+    st = getattr(L, name + "GetWorkspaceSize")(*args, ctypes.byref(ws), ctypes.byref(ex))
+    if st != 0:
+        raise CamHipError(f"{name}GetWorkspaceSize failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+    buf = None
+    if ws.value > 0:
+        buf = torch.empty(ws.value, dtype=torch.uint8, device=device)
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    st = getattr(L, name)(buf.data_ptr() if buf is not None else None, ws.value, ex, stream)
+    if st != 0:
+        raise CamHipError(f"{name} failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+    return buf

@@ -1,0 +1,127 @@
+// C1: weighted unpermute (combine).
+//   out[t] = bf16_rne( sum_{k ascending} float(y[row(t,k)]) * w[t,k] )
+// fp32 accumulation starting from +0, multiply then add, never fused
+// (moe_combine_normal.h:343-377; cam_moe_distribute_combine.h:654-716).
+//
+// Two launches:
+//   1. combine_scatter_kernel: inv[t*K+k] = row for every received row
+//      (the single-rank form of CopyBufferToShare, moe_combine_normal.h:286-303,
+//      which moves whole rows; here only the 4-byte row index moves).
+//   2. combine_gather_kernel: one wave per token reads its K rows with
+//      16-byte loads (all K loads of an iteration in flight together),
+//      accumulates in k order and writes the bf16 row once.
+// inv needs no clearing: the gather accepts inv[t*K+k] = r only when
+// 0 <= r < rows and expand_idx[r] names (t,k) back, so stale workspace
+// contents can never select a row; such slots are skipped, as the fused
+// combine skips expert ids < 0.
+#include "cam_device.h"
+#include "launchers.h"
+
+namespace cam {
+
+constexpr int COMB_WAVES = 4;
+constexpr int COMB_NIT = 7;   // H <= 7168
+constexpr int COMB_KB = 8;    // rows in flight per batch
+
+__global__ void combine_scatter_kernel(const int32_t *__restrict__ expand_idx, int N,
+                                       const int32_t *__restrict__ recv_count_last, int T, int K,
+                                       int32_t *__restrict__ inv)
+{
+    const int lim = recv_count_last ? min(N, *recv_count_last) : N;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < lim; r += gridDim.x * blockDim.x) {
+        const int t = expand_idx[(size_t)r * 3 + 1], k = expand_idx[(size_t)r * 3 + 2];
+        if (t >= 0 && t < T && k >= 0 && k < K)
+            inv[(size_t)t * K + k] = r;
+    }
+}
+
+__global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
+    const uint16_t *__restrict__ y, const int32_t *__restrict__ expand_idx, int N,
+    const int32_t *__restrict__ recv_count_last, const float *__restrict__ topk_w, int T, int K, int H,
+    uint16_t *__restrict__ out, const int32_t *__restrict__ inv)
+{
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * COMB_WAVES + (threadIdx.x >> 6);
+    if (t >= T)
+        return;
+    const int lim = recv_count_last ? min(N, *recv_count_last) : N;
+    int row = -1;
+    float w = 0.0f;
+    if (lane < K) {
+        const int r = inv[(size_t)t * K + lane];
+        if (r >= 0 && r < lim && expand_idx[(size_t)r * 3 + 1] == t && expand_idx[(size_t)r * 3 + 2] == lane) {
+            row = r;
+            w = topk_w[(size_t)t * K + lane];
+        }
+    }
+    u32x4 *orow = reinterpret_cast<u32x4 *>(out + (size_t)t * H);
+#pragma unroll 1
+    for (int j = 0; j < COMB_NIT; ++j) {
+        const int col = j * 1024 + lane * 16;
+        if (j * 1024 >= H)
+            break;
+        const bool act = col < H;
+        float acc[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            acc[i] = 0.0f;
+        for (int k0 = 0; k0 < K; k0 += COMB_KB) {
+            u32x4 v[COMB_KB][2];
+            int rk[COMB_KB];
+            float wk[COMB_KB];
+#pragma unroll
+            for (int b = 0; b < COMB_KB; ++b) {
+                const int k = k0 + b;
+                rk[b] = k < K ? __shfl(row, k, 64) : -1;
+                wk[b] = __shfl(w, k < K ? k : 0, 64);
+                if (rk[b] >= 0 && act) {
+                    const u32x4 *src = reinterpret_cast<const u32x4 *>(y + (size_t)rk[b] * H + col);
+                    v[b][0] = __builtin_nontemporal_load(src);
+                    v[b][1] = __builtin_nontemporal_load(src + 1);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < COMB_KB; ++b) {
+                if (rk[b] < 0 || !act)
+                    continue;
+                float f[16];
+                unpack_bf16x8(v[b][0], f);
+                unpack_bf16x8(v[b][1], f + 8);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = f[i] * wk[b];
+                    acc[i] = acc[i] + p;
+                }
+            }
+        }
+        if (act) {
+            orow[col >> 3] = pack_bf16x8(acc);
+            orow[(col >> 3) + 1] = pack_bf16x8(acc + 8);
+        }
+    }
+}
+
+hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                          const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *inv_ws, hipStream_t s)
+{
+    if (T == 0)
+        return hipSuccess;
+    if (H > COMB_NIT * 1024 || (H & 15) || K > 64)
+        return hipErrorInvalidValue;
+    if (N > 0) {
+        int blocks = (N + 255) / 256;
+        if (blocks > 2048)
+            blocks = 2048;
+        hipLaunchKernelGGL(combine_scatter_kernel, dim3(blocks), dim3(256), 0, s, expand_idx, N, recv_count_last, T,
+                           K, inv_ws);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess)
+            return err;
+    }
+    hipLaunchKernelGGL(combine_gather_kernel, dim3((T + COMB_WAVES - 1) / COMB_WAVES), dim3(COMB_WAVES * 64), 0, s, y,
+                       expand_idx, N, recv_count_last, topk_w, T, K, H, out, inv_ws);
+    return hipGetLastError();
+}
+
+}  // namespace cam

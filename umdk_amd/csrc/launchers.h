@@ -1,0 +1,47 @@
+// Internal host launchers, one per kernel family.  Not exported: the public
+// surface is the two-phase C ABI in include/camhip.h (implemented in api.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cam {
+
+enum QuantMode { QUANT_NONE = 0, QUANT_INT8_TOKEN = 2, QUANT_FP8_BLOCK = 3 };
+
+// ---- routing (route.hip)
+hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
+                        float *topk_w, hipStream_t s);
+
+// ---- dispatch layout (layout.hip)
+struct LayoutPlan {
+    int tokens_per_chunk;
+    int n_chunks;
+};
+LayoutPlan layout_plan(int T, int K);
+size_t layout_workspace_bytes(int T, int K, int E, int R);
+hipError_t launch_layout(const int64_t *topk_idx, int T, int K, int E, int R, int32_t *ntok_per_rank,
+                         int32_t *ntok_per_expert, int32_t *is_token_in_rank, int32_t *send_token_idx,
+                         void *ws, hipStream_t s);
+// int32 topk ids, used by the fused path
+hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
+                             int32_t *send_token_idx, void *ws, hipStream_t s);
+
+// ---- small utilities (notify.hip)
+hipError_t launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t s);
+
+// ---- count exchange for one rank (notify.hip)
+hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offset, int32_t *total_recv,
+                         int32_t *recv_count, int32_t *recv_offset, int32_t *max_bs,
+                         int64_t *recv_tokens_per_expert, int local_experts, hipStream_t s);
+
+// ---- permute + quantise (dispatch.hip)
+hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
+                           const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int quant_mode,
+                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s);
+
+// ---- weighted unpermute (combine.hip)
+hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                          const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *inv_ws,
+                          hipStream_t s);
+
+}  // namespace cam

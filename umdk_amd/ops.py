@@ -1,0 +1,184 @@
+"""torch.ops.umdk_cam_op_lib -- CAM's operator surface on MI355X.
+
+Same library name, op names, argument names, order and defaults as the
+reference's TORCH_LIBRARY block (src/cam/comm_operator/pybind/pybind.cpp:21-36),
+registered for the GPU dispatch key and backed by libcamhip.so through its C
+ABI.  Like the reference bindings (pybind/get_dispatch_layout.cpp:33-60,
+moe_dispatch_prefill.cpp:38-127, moe_combine_prefill.cpp:28-64), each op
+casts index/weight dtypes, checks shapes, allocates outputs and launches on
+the current stream; a failed check raises RuntimeError, as TORCH_BIND_ASSERT
+raises TorchBindException (torch_bind_exception.h:20-40).
+
+Differences, all documented in the op docstrings:
+  * num_ranks must be 1 (one EP rank per GPU, no collectives); the reference
+    requires 2..384.
+  * moe_dispatch_prefill takes an extra trailing `quant_mode` (default -1 =
+    follow use_quant as the reference does: 2 if use_quant else 0); 3 selects
+    FP8 e4m3fn rows with [rows, hidden/128] fp32 block scales.
+  * moe_route (routing) and grouped expert GEMM ops are additions with no
+    reference counterpart.
+"""
+import torch
+
+from . import _lib
+
+LIB_NAME = "umdk_cam_op_lib"
+
+_def = torch.library.Library(LIB_NAME, "DEF")
+_def.define("get_dispatch_layout(Tensor topk_idx, int num_experts, int num_ranks) -> (Tensor, Tensor)")
+_def.define(
+    "moe_dispatch_prefill(Tensor x, Tensor topk_idx, Tensor topk_weights, Tensor num_tokens_per_expert, "
+    "Tensor send_token_idx_small, str group_ep, int rank, int num_ranks, bool use_quant, int quant_mode=-1) "
+    "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+_def.define(
+    "moe_combine_prefill(Tensor x, Tensor topk_idx, Tensor topk_weights, Tensor src_idx, Tensor send_head, "
+    "str group_ep, int rank, int num_ranks) -> Tensor")
+_def.define("moe_route(Tensor logits, Tensor? bias, int topk) -> (Tensor, Tensor)")
+
+_impl = torch.library.Library(LIB_NAME, "IMPL", "CUDA")
+
+QUANT_NONE, QUANT_INT8_TOKEN, QUANT_FP8_BLOCK = 0, 2, 3
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _single_rank(rank, num_ranks, op):
+    _check(num_ranks == 1 and rank == 0,
+           f"{op}: this build runs one EP rank per GPU without collectives; "
+           f"num_ranks must be 1 and rank 0 (got num_ranks={num_ranks}, rank={rank})")
+
+
+def get_dispatch_layout(topk_idx, num_experts, num_ranks):
+    """Per-expert token counts and stable per-expert rank of every (t,k).
+
+    Mirrors GetDispatchLayoutImplNpu (pybind/get_dispatch_layout.cpp:33-60):
+    returns (num_tokens_per_expert [E] int32, send_token_idx [T,K] int32)."""
+    ti = topk_idx if topk_idx.dtype == torch.int64 else topk_idx.to(torch.int64)
+    _check(ti.dim() == 2, "get_dispatch_layout: topk_idx must be 2-D")
+    _check(ti.is_contiguous(), "get_dispatch_layout: topk_idx must be contiguous")
+    _check(num_experts > 0, "get_dispatch_layout: num_experts must be > 0")
+    T, K = ti.shape
+    dev = ti.device
+    nte = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    sti = torch.empty((T, K), dtype=torch.int32, device=dev)
+    _lib.call("camhipDispatchLayout", _lib.ptr(ti), T, num_ranks, num_experts, K, None, _lib.ptr(nte), None,
+              _lib.ptr(sti), device=dev)
+    return nte, sti
+
+
+def _notify(num_tokens_per_expert, T, device):
+    E = num_tokens_per_expert.shape[0]
+    i32 = dict(dtype=torch.int32, device=device)
+    send_offset = torch.empty(E, **i32)
+    total = torch.empty(1, **i32)
+    recv_count = torch.empty(E, **i32)
+    recv_offset = torch.empty(E, **i32)
+    max_bs = torch.empty(1, **i32)
+    rtpe = torch.empty(E, dtype=torch.int64, device=device)
+    _lib.call("camhipNotifyDispatch", _lib.ptr(num_tokens_per_expert), E, T, 1, 0, _lib.ptr(send_offset),
+              _lib.ptr(total), _lib.ptr(recv_count), _lib.ptr(recv_offset), _lib.ptr(max_bs), _lib.ptr(rtpe),
+              device=device)
+    return send_offset, total, recv_count, recv_offset, rtpe
+
+
+def moe_dispatch_prefill(x, topk_idx, topk_weights, num_tokens_per_expert, send_token_idx_small, group_ep, rank,
+                         num_ranks, use_quant, quant_mode=-1):
+    """Permute tokens by expert (with optional fused quantisation).
+
+    Mirrors MoeDispatchPrefillImplNpu (pybind/moe_dispatch_prefill.cpp:38-127):
+    count exchange, a host read of the received row count to size the outputs
+    (as the reference does at :110-111), then the dispatch kernel.  Returns
+    (expand_x [N,H], dynamic_scales, expand_idx [3N] int32, recv_count [E]
+    int32, recv_tokens_per_expert [E] int64).  quant_mode: -1 follows
+    use_quant (2 if set, else 0); 0 bf16 rows; 2 int8 rows + [N] scales; 3 fp8
+    e4m3fn rows + [N, H/128] scales."""
+    ti = topk_idx if topk_idx.dtype == torch.int32 else topk_idx.to(torch.int32)
+    if quant_mode < 0:
+        quant_mode = QUANT_INT8_TOKEN if use_quant else QUANT_NONE
+    _check(quant_mode in (QUANT_NONE, QUANT_INT8_TOKEN, QUANT_FP8_BLOCK),
+           f"moe_dispatch_prefill: quant_mode {quant_mode} not supported")
+    _check(num_tokens_per_expert.dtype == torch.int32, "moe_dispatch_prefill: num_tokens_per_expert must be int32")
+    _single_rank(rank, num_ranks, "moe_dispatch_prefill")
+    _check(x.dim() == 2 and x.is_contiguous(), "moe_dispatch_prefill: x must be 2-D and contiguous")
+    _check(x.dtype == torch.bfloat16, "moe_dispatch_prefill: x must be bfloat16")
+    _check(num_tokens_per_expert.dim() == 1 and num_tokens_per_expert.is_contiguous(),
+           "moe_dispatch_prefill: num_tokens_per_expert must be 1-D and contiguous")
+    _check(num_tokens_per_expert.shape[0] % num_ranks == 0,
+           "moe_dispatch_prefill: num_experts must be divisible by num_ranks")
+    T, H = x.shape
+    E = num_tokens_per_expert.shape[0]
+    _check(E > 0, "moe_dispatch_prefill: num_experts must be > 0")
+    _check(ti.dim() == 2 and ti.is_contiguous(), "moe_dispatch_prefill: topk_idx must be 2-D and contiguous")
+    _check(topk_weights.dim() == 2 and topk_weights.is_contiguous(),
+           "moe_dispatch_prefill: topk_weights must be 2-D and contiguous")
+    K = ti.shape[1]
+    _check(ti.shape[0] == T and send_token_idx_small.shape[0] == T, "moe_dispatch_prefill: token count mismatch")
+    _check(topk_weights.shape[1] == K and send_token_idx_small.shape[1] == K, "moe_dispatch_prefill: topk mismatch")
+    dev = x.device
+    send_offset, total, recv_count, recv_offset, rtpe = _notify(num_tokens_per_expert, T, dev)
+    n_recv = int(total.item())
+    n_rows = max(n_recv, 1)
+    if quant_mode == QUANT_NONE:
+        expand_x = torch.empty((n_rows, H), dtype=x.dtype, device=dev)
+        scales = torch.empty(n_rows, dtype=torch.float32, device=dev)
+    elif quant_mode == QUANT_INT8_TOKEN:
+        expand_x = torch.empty((n_rows, H), dtype=torch.int8, device=dev)
+        scales = torch.empty(n_rows, dtype=torch.float32, device=dev)
+    else:
+        expand_x = torch.empty((n_rows, H), dtype=torch.float8_e4m3fn, device=dev)
+        scales = torch.empty((n_rows, H // 128), dtype=torch.float32, device=dev)
+    expand_idx = torch.empty(n_rows * 3, dtype=torch.int32, device=dev)
+    sti = send_token_idx_small if send_token_idx_small.dtype == torch.int32 else send_token_idx_small.to(torch.int32)
+    _lib.call("camhipMoeDispatchNormal", _lib.ptr(x), _lib.ptr(ti), _lib.ptr(send_offset), _lib.ptr(sti.contiguous()),
+              _lib.ptr(recv_offset), _lib.ptr(recv_count), T, H, K, 1, 0, E, quant_mode, n_rows, _lib.ptr(expand_x),
+              _lib.ptr(scales), _lib.ptr(expand_idx), device=dev)
+    return expand_x, scales, expand_idx, recv_count, rtpe
+
+
+def moe_combine_prefill(x, topk_idx, topk_weights, src_idx, send_head, group_ep, rank, num_ranks):
+    """Weighted unpermute back to token order.
+
+    Mirrors MoeCombinePrefillImplNpu (pybind/moe_combine_prefill.cpp:28-64):
+    x [N,H] bf16 expert outputs in dispatch order, src_idx = expand_idx from
+    dispatch, send_head = recv_count; returns [T,H] with
+    out[t] = bf16(sum_k x[row(t,k)] * w[t,k]) accumulated in fp32."""
+    _single_rank(rank, num_ranks, "moe_combine_prefill")
+    _check(x.dim() == 2 and x.is_contiguous(), "moe_combine_prefill: x must be 2-D and contiguous")
+    _check(x.dtype == torch.bfloat16, "moe_combine_prefill: x must be bfloat16")
+    w = topk_weights if topk_weights.dtype == torch.float32 else topk_weights.to(torch.float32)
+    w = w.contiguous()
+    T, K = w.shape
+    N, H = x.shape
+    _check(src_idx.numel() >= 3 * N, "moe_combine_prefill: src_idx must hold 3 ints per row")
+    _check(src_idx.dtype == torch.int32, "moe_combine_prefill: src_idx must be int32")
+    E = send_head.shape[0]
+    out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    sh = send_head if send_head.dtype == torch.int32 else send_head.to(torch.int32)
+    _lib.call("camhipMoeCombineNormal", _lib.ptr(x), _lib.ptr(src_idx.contiguous()), N, _lib.ptr(sh.contiguous()),
+              _lib.ptr(w), T, K, H, 1, 0, E, _lib.ptr(out), device=x.device)
+    return out
+
+
+def moe_route(logits, bias, topk):
+    """Top-K routing (addition; no reference counterpart): returns
+    (topk_idx [T,K] int32, topk_weights [T,K] fp32); ties go to the lower id."""
+    _check(logits.dim() == 2 and logits.dtype == torch.float32, "moe_route: logits must be [T,E] float32")
+    lg = logits.contiguous()
+    T, E = lg.shape
+    b = None
+    if bias is not None:
+        _check(bias.dtype == torch.float32 and bias.numel() == E, "moe_route: bias must be [E] float32")
+        b = bias.contiguous()
+    idx = torch.empty((T, topk), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, topk), dtype=torch.float32, device=lg.device)
+    _lib.call("camhipMoeRoute", _lib.ptr(lg), _lib.ptr(b), T, E, topk, _lib.ptr(idx), _lib.ptr(w), device=lg.device)
+    return idx, w
+
+
+_impl.impl("get_dispatch_layout", get_dispatch_layout)
+_impl.impl("moe_dispatch_prefill", moe_dispatch_prefill)
+_impl.impl("moe_combine_prefill", moe_combine_prefill)
+_impl.impl("moe_route", moe_route)
