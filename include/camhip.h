@@ -52,6 +52,9 @@ typedef struct camhipExecutor camhipExecutor;
 
 CAMHIP_API const char *camhipGetLastErrorMsg(void);
 CAMHIP_API const char *camhipGetVersion(void);
+/* Frees an executor that will not be launched (aclnn has no counterpart: its
+ * executors are consumed by the launch call, as camhip's are). */
+CAMHIP_API void camhipReleaseExecutor(camhipExecutor *executor);
 
 /* ------------------------------------------------------------------ routing
  * No reference counterpart (CAM callers compute topk_idx themselves,

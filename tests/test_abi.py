@@ -69,7 +69,7 @@ def test_layout_null_output_is_rejected(L):
 def test_layout_workspace_size_and_short_workspace(L):
     st, ws, ex, _ = _ws(L, "camhipDispatchLayout", P, 4096, 1, 256, 8, P, P, P, P)
     assert st == 0
-    assert ws == 4 * 32 * (256 + 1)   # 32 chunks of 1024 entries, E+R counters each
+    assert ws == 4 * 128 * (256 + 1)   # 128 chunks of 256 entries, E+R counters each
     # second phase with a short workspace: rejected before any launch, executor freed
     st2 = L.camhipDispatchLayout(None, 0, ex, None)
     assert st2 == 161003 and "workspace" in L.camhipGetLastErrorMsg().decode()

@@ -42,6 +42,8 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.camhipGetLastErrorMsg.restype = ctypes.c_char_p
         L.camhipGetVersion.restype = ctypes.c_char_p
+        L.camhipReleaseExecutor.restype = None
+        L.camhipReleaseExecutor.argtypes = [_P]
         for name, sig in SIGNATURES.items():
             kinds = sig.replace(" ", "")
             f = getattr(L, name + "GetWorkspaceSize")
@@ -88,3 +90,32 @@ def call(name, *args, device=None, stream=None):
     if st != 0:
         raise CamHipError(f"{name} failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
     return buf
+
+
+def launch(name, *args, workspace=None, stream=None, device=None):
+    """Like call(), but with a caller-owned workspace tensor (no allocation:
+    safe inside a captured graph once the workspace is large enough)."""
+    L = lib()
+    ws = ctypes.c_uint64(0)
+    ex = ctypes.c_void_p(0)
+    st = getattr(L, name + "GetWorkspaceSize")(*args, ctypes.byref(ws), ctypes.byref(ex))
+    if st != 0:
+        raise CamHipError(f"{name}GetWorkspaceSize failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+    have = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    st = getattr(L, name)(workspace.data_ptr() if workspace is not None else None, have, ex, stream)
+    if st != 0:
+        raise CamHipError(f"{name} failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+
+
+def workspace_size(name, *args):
+    """First phase only; the executor is released by a zero-size second call."""
+    L = lib()
+    ws = ctypes.c_uint64(0)
+    ex = ctypes.c_void_p(0)
+    st = getattr(L, name + "GetWorkspaceSize")(*args, ctypes.byref(ws), ctypes.byref(ex))
+    if st != 0:
+        raise CamHipError(f"{name}GetWorkspaceSize failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+    L.camhipReleaseExecutor(ex)
+    return ws.value

@@ -93,6 +93,7 @@ extern "C" {
 
 const char *camhipGetLastErrorMsg(void) { return g_last_error.c_str(); }
 const char *camhipGetVersion(void) { return "camhip 0.1.0 gfx950"; }
+void camhipReleaseExecutor(camhipExecutor *executor) { delete executor; }
 
 // ---------------------------------------------------------------- routing
 camhipStatus camhipMoeRouteGetWorkspaceSize(const float *logits, const float *bias, int64_t numTokens,
@@ -233,10 +234,11 @@ camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(const uint16_t *x, const in
     }
     const int T = (int)numTokens, H = (int)hidden, K = (int)numTopk, E = (int)moeExpertNum, q = (int)quantMode;
     const int rank = (int)epRankId;
+    const int cap = recvRowsCapacity > 0x7fffffff ? 0x7fffffff : (int)recvRowsCapacity;
     return make_executor(
         0,
         [=](void *, hipStream_t s) {
-            return cam::launch_dispatch(x, topkIdx, sendOffset, sendTokenIdx, T, H, K, E, rank, q, recvX, recvXScales,
+            return cam::launch_dispatch(x, topkIdx, sendOffset, sendTokenIdx, T, H, K, E, rank, cap, q, recvX, recvXScales,
                                         assistInfoForCombine, s);
         },
         workspaceSize, executor);

@@ -7,9 +7,9 @@
 //   1. combine_scatter_kernel: inv[t*K+k] = row for every received row
 //      (the single-rank form of CopyBufferToShare, moe_combine_normal.h:286-303,
 //      which moves whole rows; here only the 4-byte row index moves).
-//   2. combine_gather_kernel: one wave per token reads its K rows with
-//      16-byte loads (all K loads of an iteration in flight together),
-//      accumulates in k order and writes the bf16 row once.
+//   2. combine_gather_kernel: one wave per (token, 1024-column chunk) reads
+//      its K row slices with 16-byte loads (all K in flight together),
+//      accumulates in k order and writes the bf16 slice once.
 // inv needs no clearing: the gather accepts inv[t*K+k] = r only when
 // 0 <= r < rows and expand_idx[r] names (t,k) back, so stale workspace
 // contents can never select a row; such slots are skipped, as the fused
@@ -37,14 +37,18 @@ __global__ void combine_scatter_kernel(const int32_t *__restrict__ expand_idx, i
 
 __global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
     const uint16_t *__restrict__ y, const int32_t *__restrict__ expand_idx, int N,
-    const int32_t *__restrict__ recv_count_last, const float *__restrict__ topk_w, int T, int K, int H,
+    const int32_t *__restrict__ recv_count_last, const float *__restrict__ topk_w, int T, int K, int H, int nchunk,
     uint16_t *__restrict__ out, const int32_t *__restrict__ inv)
 {
 #pragma clang fp contract(off)
+    // one wave per (token, 1024-column chunk): lane l owns columns [1024 j + 8 l, +8) and
+    // [1024 j + 512 + 8 l, +8), so each 16-byte load or store instruction of the wave covers
+    // one contiguous kilobyte (whole cache lines, no partial-line writes)
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * COMB_WAVES + (threadIdx.x >> 6);
-    if (t >= T)
+    const long item = (long)blockIdx.x * COMB_WAVES + (threadIdx.x >> 6);
+    if (item >= (long)T * nchunk)
         return;
+    const int t = (int)(item / nchunk), j = (int)(item % nchunk);
     const int lim = recv_count_last ? min(N, *recv_count_last) : N;
     int row = -1;
     float w = 0.0f;
@@ -55,50 +59,48 @@ __global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
             w = topk_w[(size_t)t * K + lane];
         }
     }
-    u32x4 *orow = reinterpret_cast<u32x4 *>(out + (size_t)t * H);
-#pragma unroll 1
-    for (int j = 0; j < COMB_NIT; ++j) {
-        const int col = j * 1024 + lane * 16;
-        if (j * 1024 >= H)
-            break;
-        const bool act = col < H;
-        float acc[16];
+    const int col = j * 1024 + lane * 8;
+    const bool act = col < H;         // H % 16 == 0 and 1024-aligned chunks: both halves or neither
+    const bool act1 = col + 512 < H;
+    float acc[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            acc[i] = 0.0f;
-        for (int k0 = 0; k0 < K; k0 += COMB_KB) {
-            u32x4 v[COMB_KB][2];
-            int rk[COMB_KB];
-            float wk[COMB_KB];
+    for (int i = 0; i < 16; ++i)
+        acc[i] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += COMB_KB) {
+        u32x4 v[COMB_KB][2];
+        int rk[COMB_KB];
+        float wk[COMB_KB];
 #pragma unroll
-            for (int b = 0; b < COMB_KB; ++b) {
-                const int k = k0 + b;
-                rk[b] = k < K ? __shfl(row, k, 64) : -1;
-                wk[b] = __shfl(w, k < K ? k : 0, 64);
-                if (rk[b] >= 0 && act) {
-                    const u32x4 *src = reinterpret_cast<const u32x4 *>(y + (size_t)rk[b] * H + col);
-                    v[b][0] = __builtin_nontemporal_load(src);
-                    v[b][1] = __builtin_nontemporal_load(src + 1);
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < COMB_KB; ++b) {
-                if (rk[b] < 0 || !act)
-                    continue;
-                float f[16];
-                unpack_bf16x8(v[b][0], f);
-                unpack_bf16x8(v[b][1], f + 8);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float p = f[i] * wk[b];
-                    acc[i] = acc[i] + p;
-                }
+        for (int b = 0; b < COMB_KB; ++b) {
+            const int k = k0 + b;
+            rk[b] = k < K ? __shfl(row, k, 64) : -1;
+            wk[b] = __shfl(w, k < K ? k : 0, 64);
+            if (rk[b] >= 0 && act) {
+                const uint16_t *src = y + (size_t)rk[b] * H + col;
+                v[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src));
+                v[b][1] = act1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + 512))
+                               : u32x4{0, 0, 0, 0};
             }
         }
-        if (act) {
-            orow[col >> 3] = pack_bf16x8(acc);
-            orow[(col >> 3) + 1] = pack_bf16x8(acc + 8);
+#pragma unroll
+        for (int b = 0; b < COMB_KB; ++b) {
+            if (rk[b] < 0 || !act)
+                continue;
+            float f[16];
+            unpack_bf16x8(v[b][0], f);
+            unpack_bf16x8(v[b][1], f + 8);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = f[i] * wk[b];
+                acc[i] = acc[i] + p;
+            }
         }
+    }
+    if (act) {
+        uint16_t *orow = out + (size_t)t * H + col;
+        __builtin_nontemporal_store(pack_bf16x8(acc), reinterpret_cast<u32x4 *>(orow));
+        if (act1)
+            __builtin_nontemporal_store(pack_bf16x8(acc + 8), reinterpret_cast<u32x4 *>(orow + 512));
     }
 }
 
@@ -119,8 +121,11 @@ hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, c
         if (err != hipSuccess)
             return err;
     }
-    hipLaunchKernelGGL(combine_gather_kernel, dim3((T + COMB_WAVES - 1) / COMB_WAVES), dim3(COMB_WAVES * 64), 0, s, y,
-                       expand_idx, N, recv_count_last, topk_w, T, K, H, out, inv_ws);
+    const int nchunk = (H + 1023) / 1024;
+    const long items = (long)T * nchunk;
+    hipLaunchKernelGGL(combine_gather_kernel, dim3((unsigned)((items + COMB_WAVES - 1) / COMB_WAVES)),
+                       dim3(COMB_WAVES * 64), 0, s, y, expand_idx, N, recv_count_last, topk_w, T, K, H, nchunk, out,
+                       inv_ws);
     return hipGetLastError();
 }
 

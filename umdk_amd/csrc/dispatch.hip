@@ -2,11 +2,12 @@
 // Row of (t,k) = send_offset[e] + send_token_idx[t,k]  (moe_dispatch_normal.h:381-398)
 // expand_idx[row] = (rank, t, k)                       (moe_dispatch_normal.h:335-344)
 //
-// One wave per token.  The wave reads the token's row once (16-byte loads,
-// lane l owns elements [1024 j + 16 l, +16) of iteration j), quantises it
-// once in registers, and writes the same bytes to each of the token's K
-// destination rows as 16-byte stores: HBM traffic is one read of x and one
-// write per routed row, the algorithmic minimum.
+// One wave per (token, 1024-column chunk) for bf16 and fp8 rows (one wave
+// per token for int8, whose scale needs the whole row).  The wave reads its
+// slice of the token's row once (16-byte loads, lane l owns columns
+// [1024 j + 16 l, +16)), quantises it once in registers, and writes the same
+// bytes to each of the token's K destination rows as 16-byte stores: HBM
+// traffic is one read of x and one write per routed row, the minimum.
 //   quant_mode 0: bf16 copy.
 //   quant_mode 2: int8 per token, s = 127/(amax+1e-12), q = rint(x*s), scale = 1/s
 //                 (moe_dispatch_normal.h:295-332).
@@ -23,26 +24,121 @@ constexpr int DISP_WAVES = 4;
 constexpr int DISP_NIT = 7;  // H <= 7168 = 7 * 1024
 constexpr int DISP_MAX_K = 16;
 
+// Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
+__device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
+                                             const int32_t *__restrict__ send_offset,
+                                             const int32_t *__restrict__ send_token_idx, int t, int K, int E,
+                                             int cap, int lane)
+{
+    int dst = -1;
+    if (lane < K) {
+        const int e = topk_idx[(size_t)t * K + lane];
+        if (e >= 0 && e < E) {
+            dst = send_offset[e] + send_token_idx[(size_t)t * K + lane];
+            if (dst < 0 || dst >= cap)  // inconsistent counts: never write outside the output
+                dst = -1;
+        }
+    }
+    return dst;
+}
+
+// bf16 copy and fp8 1x128 quantisation: one wave per (token, 1024-column chunk).
 template <int MODE>
-__global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_kernel(
+__global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
-    const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, uint8_t *__restrict__ expand_x,
-    float *__restrict__ scales, int32_t *__restrict__ expand_idx)
+    const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap, int nchunk,
+    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx)
+{
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const long item = (long)blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
+    if (item >= (long)T * nchunk)
+        return;
+    const int t = (int)(item / nchunk), j = (int)(item % nchunk);
+    const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
+    if constexpr (MODE == QUANT_NONE) {
+        // lane l copies columns [1024 j + 8 l, +8) and [1024 j + 512 + 8 l, +8): each 16-byte
+        // store instruction of the wave writes one contiguous kilobyte
+        const int col = j * 1024 + lane * 8;
+        const bool act = col < H, act1 = col + 512 < H;
+        u32x4 raw0 = u32x4{0, 0, 0, 0}, raw1 = u32x4{0, 0, 0, 0};
+        if (act) {
+            raw0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col));
+            if (act1)
+                raw1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col + 512));
+        }
+        for (int k = 0; k < K; ++k) {
+            const int row = __shfl(dst, k, 64);
+            if (row < 0)
+                continue;
+            if (act) {
+                uint16_t *out = reinterpret_cast<uint16_t *>(expand_x) + (size_t)row * H + col;
+                *reinterpret_cast<u32x4 *>(out) = raw0;
+                if (act1)
+                    *reinterpret_cast<u32x4 *>(out + 512) = raw1;
+            }
+            if (j == 0 && lane == 0) {
+                expand_idx[(size_t)row * 3 + 0] = rank;
+                expand_idx[(size_t)row * 3 + 1] = t;
+                expand_idx[(size_t)row * 3 + 2] = k;
+            }
+        }
+    } else {
+        // lane l quantises columns [1024 j + 16 l, +16): one 16-byte fp8 store per row
+        const int col = j * 1024 + lane * 16;
+        const bool act = col < H;
+        u32x4 raw0 = u32x4{0, 0, 0, 0}, raw1 = u32x4{0, 0, 0, 0};
+        if (act) {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col);
+            raw0 = __builtin_nontemporal_load(src);
+            raw1 = __builtin_nontemporal_load(src + 1);
+        }
+        float f[16];
+        unpack_bf16x8(raw0, f);
+        unpack_bf16x8(raw1, f + 8);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            amax = fmaxf(amax, fabsf(f[i]));
+        amax = fmaxf(group_max<8>(amax), 1e-4f);  // a 128-block is 8 adjacent lanes
+        const float inv = 448.0f / amax;
+        const float bscale = amax / 448.0f;
+        u32x4 q;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            q[w] = f32x4_to_e4m3(f[4 * w] * inv, f[4 * w + 1] * inv, f[4 * w + 2] * inv, f[4 * w + 3] * inv);
+        const int nb = H >> 7;
+        for (int k = 0; k < K; ++k) {
+            const int row = __shfl(dst, k, 64);
+            if (row < 0)
+                continue;
+            if (act) {
+                *reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H + col) = q;
+                if ((lane & 7) == 0)
+                    scales[(size_t)row * nb + (col >> 7)] = bscale;
+            }
+            if (j == 0 && lane == 0) {
+                expand_idx[(size_t)row * 3 + 0] = rank;
+                expand_idx[(size_t)row * 3 + 1] = t;
+                expand_idx[(size_t)row * 3 + 2] = k;
+            }
+        }
+    }
+}
+
+// int8 per-token quantisation needs the whole row's amax: one wave per token,
+// the row held in registers (lane l owns columns [1024 j + 16 l, +16)).
+__global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
+    const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
+    const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap,
+    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
     if (t >= T)
         return;
-
-    // destinations: lane k < K resolves entry (t,k)
-    int dst = -1;
-    if (lane < K) {
-        const int e = topk_idx[(size_t)t * K + lane];
-        if (e >= 0 && e < E)
-            dst = send_offset[e] + send_token_idx[(size_t)t * K + lane];
-    }
-
+    const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
     const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)t * H);
     u32x4 raw[DISP_NIT][2];
 #pragma unroll
@@ -56,133 +152,82 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_kernel(
             raw[j][1] = u32x4{0, 0, 0, 0};
         }
     }
-
-    if constexpr (MODE == QUANT_NONE) {
-        for (int k = 0; k < K; ++k) {
-            const int row = __shfl(dst, k, 64);
-            if (row < 0)
-                continue;
-            u32x4 *out = reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H * 2);
+    float amax = 0.0f;
 #pragma unroll
-            for (int j = 0; j < DISP_NIT; ++j) {
-                const int col = j * 1024 + lane * 16;
-                if (col < H) {
-                    out[(col >> 3)] = raw[j][0];
-                    out[(col >> 3) + 1] = raw[j][1];
-                }
+    for (int j = 0; j < DISP_NIT; ++j) {
+        float f[16];
+        unpack_bf16x8(raw[j][0], f);
+        unpack_bf16x8(raw[j][1], f + 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            amax = fmaxf(amax, fabsf(f[i]));
+    }
+    amax = group_max<64>(amax);
+    const float sc = 127.0f / (amax + 1e-12f);
+    const float tok_scale = 1.0f / sc;
+    u32x4 q[DISP_NIT];
+#pragma unroll
+    for (int j = 0; j < DISP_NIT; ++j) {
+        float f[16];
+        unpack_bf16x8(raw[j][0], f);
+        unpack_bf16x8(raw[j][1], f + 8);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t pk = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int v = (int)rintf(f[4 * w + b] * sc);
+                pk |= (uint32_t)(v & 0xff) << (8 * b);
             }
-            if (lane == 0) {
-                expand_idx[(size_t)row * 3 + 0] = rank;
-                expand_idx[(size_t)row * 3 + 1] = t;
-                expand_idx[(size_t)row * 3 + 2] = k;
-            }
+            q[j][w] = pk;
         }
-    } else {
-        u32x4 q[DISP_NIT];
-        float blk_scale[DISP_NIT];
-        float tok_scale = 0.0f;
-        if constexpr (MODE == QUANT_INT8_TOKEN) {
-            float amax = 0.0f;
+    }
+    for (int k = 0; k < K; ++k) {
+        const int row = __shfl(dst, k, 64);
+        if (row < 0)
+            continue;
+        u32x4 *out = reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H);
 #pragma unroll
-            for (int j = 0; j < DISP_NIT; ++j) {
-                float f[16];
-                unpack_bf16x8(raw[j][0], f);
-                unpack_bf16x8(raw[j][1], f + 8);
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    amax = fmaxf(amax, fabsf(f[i]));
-            }
-            amax = group_max<64>(amax);
-            const float sc = 127.0f / (amax + 1e-12f);
-            tok_scale = 1.0f / sc;
-#pragma unroll
-            for (int j = 0; j < DISP_NIT; ++j) {
-                float f[16];
-                unpack_bf16x8(raw[j][0], f);
-                unpack_bf16x8(raw[j][1], f + 8);
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    uint32_t pk = 0;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int v = (int)rintf(f[4 * w + b] * sc);
-                        pk |= (uint32_t)(v & 0xff) << (8 * b);
-                    }
-                    q[j][w] = pk;
-                }
-                blk_scale[j] = 0.0f;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < DISP_NIT; ++j) {
-                float f[16];
-                unpack_bf16x8(raw[j][0], f);
-                unpack_bf16x8(raw[j][1], f + 8);
-                float amax = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    amax = fmaxf(amax, fabsf(f[i]));
-                amax = fmaxf(group_max<8>(amax), 1e-4f);
-                const float inv = 448.0f / amax;
-                blk_scale[j] = amax / 448.0f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    q[j][w] = f32x4_to_e4m3(f[4 * w] * inv, f[4 * w + 1] * inv, f[4 * w + 2] * inv,
-                                            f[4 * w + 3] * inv);
-            }
+        for (int j = 0; j < DISP_NIT; ++j) {
+            const int col = j * 1024 + lane * 16;
+            if (col < H)
+                out[col >> 4] = q[j];
         }
-        const int nb = H >> 7;
-        for (int k = 0; k < K; ++k) {
-            const int row = __shfl(dst, k, 64);
-            if (row < 0)
-                continue;
-            u32x4 *out = reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H);
-#pragma unroll
-            for (int j = 0; j < DISP_NIT; ++j) {
-                const int col = j * 1024 + lane * 16;
-                if (col < H) {
-                    out[col >> 4] = q[j];
-                    if constexpr (MODE == QUANT_FP8_BLOCK) {
-                        if ((lane & 7) == 0)
-                            scales[(size_t)row * nb + (col >> 7)] = blk_scale[j];
-                    }
-                }
-            }
-            if (lane == 0) {
-                if constexpr (MODE == QUANT_INT8_TOKEN)
-                    scales[row] = tok_scale;
-                expand_idx[(size_t)row * 3 + 0] = rank;
-                expand_idx[(size_t)row * 3 + 1] = t;
-                expand_idx[(size_t)row * 3 + 2] = k;
-            }
+        if (lane == 0) {
+            scales[row] = tok_scale;
+            expand_idx[(size_t)row * 3 + 0] = rank;
+            expand_idx[(size_t)row * 3 + 1] = t;
+            expand_idx[(size_t)row * 3 + 2] = k;
         }
     }
 }
 
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
-                           const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int quant_mode,
+                           const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s)
 {
     if (T == 0)
         return hipSuccess;
     if (H > DISP_NIT * 1024 || K > DISP_MAX_K || (H & 15))
         return hipErrorInvalidValue;
-    const dim3 grid((T + DISP_WAVES - 1) / DISP_WAVES), block(DISP_WAVES * 64);
+    const dim3 block(DISP_WAVES * 64);
+    const int nchunk = (H + 1023) / 1024;
+    const dim3 grid_chunk((unsigned)(((long)T * nchunk + DISP_WAVES - 1) / DISP_WAVES));
     uint8_t *ex = (uint8_t *)expand_x;
     switch (quant_mode) {
     case QUANT_NONE:
-        hipLaunchKernelGGL(dispatch_kernel<QUANT_NONE>, grid, block, 0, s, x, topk_idx, send_offset, send_token_idx,
-                           T, H, K, E, rank, ex, scales, expand_idx);
+        hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_NONE>, grid_chunk, block, 0, s, x, topk_idx, send_offset,
+                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx);
         break;
     case QUANT_INT8_TOKEN:
-        hipLaunchKernelGGL(dispatch_kernel<QUANT_INT8_TOKEN>, grid, block, 0, s, x, topk_idx, send_offset,
-                           send_token_idx, T, H, K, E, rank, ex, scales, expand_idx);
+        hipLaunchKernelGGL(dispatch_int8_kernel, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x, topk_idx,
+                           send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx);
         break;
     case QUANT_FP8_BLOCK:
         if (H & 127)
             return hipErrorInvalidValue;
-        hipLaunchKernelGGL(dispatch_kernel<QUANT_FP8_BLOCK>, grid, block, 0, s, x, topk_idx, send_offset,
-                           send_token_idx, T, H, K, E, rank, ex, scales, expand_idx);
+        hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_FP8_BLOCK>, grid_chunk, block, 0, s, x, topk_idx,
+                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx);
         break;
     default:
         return hipErrorInvalidValue;

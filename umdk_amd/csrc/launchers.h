@@ -36,7 +36,7 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
 
 // ---- permute + quantise (dispatch.hip)
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
-                           const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int quant_mode,
+                           const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s);
 
 // ---- weighted unpermute (combine.hip)

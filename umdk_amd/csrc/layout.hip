@@ -3,24 +3,27 @@
 // per-expert and per-rank token counts and the token->rank membership table.
 // Restates dispatch_layout.h:112-161 (count, cross-core prefix, rank).
 //
-// Two launches over token-aligned chunks of about 1024 (t,k) entries:
+// Three launches over token-aligned chunks of at most 256 (t,k) entries:
 //   1. layout_hist_kernel: per-chunk expert/rank histograms (LDS atomics;
-//      order does not matter for counts) and is_token_in_rank rows.
-//   2. layout_rank_kernel: each chunk sums the histograms of the chunks
-//      before it (its per-expert base), then ranks its entries in order,
-//      512 at a time: within a wave the lanes sharing an expert are found
-//      with one ballot per bit of the expert id, and waves are ordered
-//      through per-wave counts in LDS.  No atomics decide an order, so the
-//      result is deterministic and identical to the serial loop.
+//      order does not matter for counts) and is_token_in_rank rows, stored
+//      transposed: counts[e][chunk].
+//   2. layout_scan_kernel: one wave per expert (and per rank) turns its row
+//      of chunk counts into exclusive chunk bases (wave prefix scan) and
+//      writes the totals.
+//   3. layout_rank_kernel: one block per chunk ranks its entries in order:
+//      within a wave the lanes sharing an expert are found with one ballot
+//      per bit of the expert id, and waves are ordered through per-wave
+//      counts in LDS.  No atomics decide an order, so the result is
+//      deterministic and identical to the serial loop.
 // Expert ids outside [0,E) are not routed: send_token_idx = -1, not counted.
 #include "cam_device.h"
 #include "launchers.h"
 
 namespace cam {
 
-constexpr int CHUNK_ENTRIES = 1024;
+constexpr int CHUNK_ENTRIES = 256;
 constexpr int HIST_THREADS = 256;
-constexpr int RANK_THREADS = 512;
+constexpr int RANK_THREADS = 256;
 constexpr int RANK_WAVES = RANK_THREADS / 64;
 constexpr int MAX_E = 512;
 constexpr int MAX_R = 384;
@@ -43,25 +46,23 @@ template <typename IdxT>
 __global__ __launch_bounds__(HIST_THREADS) void layout_hist_kernel(const IdxT *__restrict__ topk_idx, int T, int K,
                                                                    int E, int R, int tpc,
                                                                    int32_t *__restrict__ is_token_in_rank,
-                                                                   int32_t *__restrict__ chunk_counts)
+                                                                   int32_t *__restrict__ counts)
 {
     __shared__ int32_t hist[MAX_E + MAX_R];
     int32_t *rhist = hist + E;
     for (int i = threadIdx.x; i < E + R; i += HIST_THREADS)
         hist[i] = 0;
     __syncthreads();
-    const int c = blockIdx.x;
+    const int c = blockIdx.x, nc = gridDim.x;
     const int t0 = c * tpc, t1 = min(T, t0 + tpc);
     const int per_rank = E / R;
-    for (int t = t0 + threadIdx.x; t < t1; t += HIST_THREADS) {
+    // entries of the chunk, one per thread (tpc*K <= 256)
+    const int i = threadIdx.x;
+    const int t = t0 + i / K, k = i % K;
+    if (t < t1) {
         const IdxT *row = topk_idx + (size_t)t * K;
-        if (is_token_in_rank)
-            for (int r = 0; r < R; ++r)
-                is_token_in_rank[(size_t)t * R + r] = 0;
-        for (int k = 0; k < K; ++k) {
-            const int64_t e = row[k];
-            if (e < 0 || e >= E)
-                continue;
+        const int64_t e = row[k];
+        if (e >= 0 && e < E) {
             atomicAdd(&hist[e], 1);
             const int r = (int)e / per_rank;
             bool first = true;
@@ -70,90 +71,103 @@ __global__ __launch_bounds__(HIST_THREADS) void layout_hist_kernel(const IdxT *_
                 if (ee >= 0 && ee < E && (int)ee / per_rank == r)
                     first = false;
             }
-            if (first) {
+            if (first)
                 atomicAdd(&rhist[r], 1);
-                if (is_token_in_rank)
-                    is_token_in_rank[(size_t)t * R + r] = 1;
+        }
+    }
+    if (is_token_in_rank) {
+        // rows of this chunk's tokens: 0/1 membership, written once each
+        for (long q = threadIdx.x; q < (long)(t1 - t0) * R; q += HIST_THREADS) {
+            const int tt = t0 + (int)(q / R), r = (int)(q % R);
+            const IdxT *row = topk_idx + (size_t)tt * K;
+            int in = 0;
+            for (int kk = 0; kk < K; ++kk) {
+                const int64_t ee = row[kk];
+                in |= (ee >= 0 && ee < E && (int)ee / per_rank == r);
             }
+            is_token_in_rank[(size_t)tt * R + r] = in;
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < E + R; i += HIST_THREADS)
-        chunk_counts[(size_t)c * (E + R) + i] = hist[i];
+    for (int q = threadIdx.x; q < E + R; q += HIST_THREADS)
+        counts[(size_t)q * nc + c] = hist[q];
+}
+
+// One wave per counter row (experts, then ranks): exclusive scan over chunks.
+__global__ __launch_bounds__(256) void layout_scan_kernel(int E, int R, int nc, int32_t *__restrict__ counts,
+                                                          int32_t *__restrict__ ntok_per_expert,
+                                                          int32_t *__restrict__ ntok_per_rank)
+{
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (q >= E + R)
+        return;
+    int32_t *row = counts + (size_t)q * nc;
+    int32_t carry = 0;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int c = c0 + lane;
+        const int32_t v = c < nc ? row[c] : 0;
+        int32_t incl = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t u = __shfl_up(incl, o, 64);
+            if (lane >= o)
+                incl += u;
+        }
+        if (c < nc)
+            row[c] = carry + incl - v;
+        carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) {
+        if (q < E) {
+            if (ntok_per_expert)
+                ntok_per_expert[q] = carry;
+        } else if (ntok_per_rank) {
+            ntok_per_rank[q - E] = carry;
+        }
+    }
 }
 
 template <typename IdxT>
 __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *__restrict__ topk_idx, int T, int K,
-                                                                   int E, int R, int tpc,
-                                                                   const int32_t *__restrict__ chunk_counts,
-                                                                   int32_t *__restrict__ ntok_per_expert,
-                                                                   int32_t *__restrict__ ntok_per_rank,
+                                                                   int E, int tpc,
+                                                                   const int32_t *__restrict__ chunk_base,
                                                                    int32_t *__restrict__ send_token_idx)
 {
-    __shared__ int32_t run[MAX_E];
     __shared__ int32_t wave_hist[RANK_WAVES][MAX_E];
-    const int c = blockIdx.x;
-    const int nc = gridDim.x;
-    const int ER = E + R;
-    for (int e = threadIdx.x; e < E; e += RANK_THREADS) {
-        int32_t base = 0;
-        for (int cc = 0; cc < c; ++cc)
-            base += chunk_counts[(size_t)cc * ER + e];
-        run[e] = base;
-        if (c == nc - 1 && ntok_per_expert)
-            ntok_per_expert[e] = base + chunk_counts[(size_t)c * ER + e];
-    }
-    if (c == nc - 1 && ntok_per_rank)
-        for (int r = threadIdx.x; r < R; r += RANK_THREADS) {
-            int32_t tot = 0;
-            for (int cc = 0; cc < nc; ++cc)
-                tot += chunk_counts[(size_t)cc * ER + E + r];
-            ntok_per_rank[r] = tot;
-        }
-    const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+    const int c = blockIdx.x, nc = gridDim.x;
     const int w = threadIdx.x >> 6;
-    const uint64_t lt = lanemask_lt();
+    for (int j = threadIdx.x; j < RANK_WAVES * E; j += RANK_THREADS)
+        wave_hist[j / E][j % E] = 0;
+    __syncthreads();
     const long i0 = (long)c * tpc * K;
     const long i1 = (long)min(T, (c + 1) * tpc) * K;
-    for (long base = i0; base < i1; base += RANK_THREADS) {
-        for (int j = threadIdx.x; j < RANK_WAVES * E; j += RANK_THREADS)
-            (&wave_hist[0][0])[(j / E) * MAX_E + (j % E)] = 0;
-        __syncthreads();
-        const long i = base + threadIdx.x;
-        int e = -1;
-        if (i < i1) {
-            const int64_t v = topk_idx[i];
-            e = (v >= 0 && v < E) ? (int)v : -1;
+    const long i = i0 + threadIdx.x;   // tpc*K <= RANK_THREADS: one entry per thread
+    int e = -1;
+    if (i < i1) {
+        const int64_t v = topk_idx[i];
+        e = (v >= 0 && v < E) ? (int)v : -1;
+    }
+    const bool valid = e >= 0;
+    const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = valid && ((e >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    const int inrank = __popcll(peers & lanemask_lt());
+    if (valid && inrank == 0)
+        wave_hist[w][e] = __popcll(peers);
+    __syncthreads();
+    if (i < i1) {
+        int32_t rank = -1;
+        if (valid) {
+            rank = chunk_base[(size_t)e * nc + c] + inrank;
+            for (int ww = 0; ww < w; ++ww)
+                rank += wave_hist[ww][e];
         }
-        const bool valid = e >= 0;
-        uint64_t peers = __ballot(valid);
-        for (int b = 0; b < nbits; ++b) {
-            const bool bit = valid && ((e >> b) & 1);
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
-        }
-        const int inrank = __popcll(peers & lt);
-        if (valid && inrank == 0)
-            wave_hist[w][e] = __popcll(peers);
-        __syncthreads();
-        if (i < i1) {
-            int32_t rank = -1;
-            if (valid) {
-                rank = run[e] + inrank;
-                for (int ww = 0; ww < w; ++ww)
-                    rank += wave_hist[ww][e];
-            }
-            send_token_idx[i] = rank;
-        }
-        __syncthreads();
-        for (int ee = threadIdx.x; ee < E; ee += RANK_THREADS) {
-            int32_t s = 0;
-#pragma unroll
-            for (int ww = 0; ww < RANK_WAVES; ++ww)
-                s += wave_hist[ww][ee];
-            run[ee] += s;
-        }
-        __syncthreads();
+        send_token_idx[i] = rank;
     }
 }
 
@@ -173,14 +187,19 @@ static hipError_t layout_impl(const IdxT *topk_idx, int T, int K, int E, int R, 
             err = launch_fill_i32(ntok_per_rank, 0, R, s);
         return err;
     }
-    int32_t *chunk_counts = (int32_t *)ws;
+    int32_t *counts = (int32_t *)ws;
     hipLaunchKernelGGL((layout_hist_kernel<IdxT>), dim3(p.n_chunks), dim3(HIST_THREADS), 0, s, topk_idx, T, K, E, R,
-                       p.tokens_per_chunk, is_token_in_rank, chunk_counts);
+                       p.tokens_per_chunk, is_token_in_rank, counts);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
         return err;
-    hipLaunchKernelGGL((layout_rank_kernel<IdxT>), dim3(p.n_chunks), dim3(RANK_THREADS), 0, s, topk_idx, T, K, E, R,
-                       p.tokens_per_chunk, chunk_counts, ntok_per_expert, ntok_per_rank, send_token_idx);
+    hipLaunchKernelGGL(layout_scan_kernel, dim3((E + R + 3) / 4), dim3(256), 0, s, E, R, p.n_chunks, counts,
+                       ntok_per_expert, ntok_per_rank);
+    err = hipGetLastError();
+    if (err != hipSuccess)
+        return err;
+    hipLaunchKernelGGL((layout_rank_kernel<IdxT>), dim3(p.n_chunks), dim3(RANK_THREADS), 0, s, topk_idx, T, K, E,
+                       p.tokens_per_chunk, counts, send_token_idx);
     return hipGetLastError();
 }
 

@@ -1,7 +1,12 @@
-// R0: top-K routing.  One wave per token; experts are spread over the 64
-// lanes (lane l holds experts l, l+64, ...).  Each of the K rounds is a wave
-// arg-max on (score, -index), so ties go to the lower expert id.  Gates are
-// softmax(logits) at the selected experts, renormalised over the K picks:
+// R0: top-K routing.  A token is handled by a 16-lane row of a wave (four
+// tokens per wave); lane l of the row holds experts l, l+16, l+32, ...
+// Each (score, expert) pair is a 64-bit key: the score's bits mapped to an
+// order-preserving unsigned integer, then ~expert, so the largest key is the
+// largest score with ties going to the lower expert id.  Each of the K
+// rounds takes the row-wide maximum key with four DPP steps (quad xor 1,
+// quad xor 2, half-row mirror, row mirror) -- no LDS traffic -- and the
+// owning lane retires that expert.
+// Gates are softmax(logits) at the picks renormalised over the K picks:
 // w_k = exp(l_k - max_l) / sum_j exp(l_j - max_l), summed in pick order.
 // There is no reference routing kernel (callers pass topk_idx; see
 // src/cam/examples/moe_dispatch_combine_prefill_sample.py:87-93).
@@ -10,81 +15,101 @@
 
 namespace cam {
 
-constexpr int ROUTE_MAX_PER_LANE = 8;  // E <= 512
 constexpr int ROUTE_WAVES = 4;
+constexpr int ROUTE_MAX_PER_LANE = 32;  // E <= 512 over 16 lanes
 
+// dpp_ctrl codes (GCN/CDNA DPP): quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror
+constexpr int DPP_QUAD_XOR1 = 0xB1;
+constexpr int DPP_QUAD_XOR2 = 0x4E;
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+
+template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL> __device__ __forceinline__ void key_max_step(uint32_t &hi, uint32_t &lo)
+{
+    const uint32_t ohi = dpp<CTRL>(hi), olo = dpp<CTRL>(lo);
+    if (ohi > hi || (ohi == hi && olo > lo)) {
+        hi = ohi;
+        lo = olo;
+    }
+}
+
+template <int CTRL> __device__ __forceinline__ float fmax_step(float v)
+{
+    return fmaxf(v, __uint_as_float(dpp<CTRL>(__float_as_uint(v))));
+}
+
+__device__ __forceinline__ uint32_t order_key(float s)
+{
+    const uint32_t u = __float_as_uint(s);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int PER>
 __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int T, int E,
                                                                  int K, int32_t *__restrict__ topk_idx,
                                                                  float *__restrict__ topk_w)
 {
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6);
-    if (t >= T)
-        return;
-    const float *l = logits + (size_t)t * E;
-    float lg[ROUTE_MAX_PER_LANE], sc[ROUTE_MAX_PER_LANE];
+    const int l16 = lane & 15;
+    const int t = (blockIdx.x * ROUTE_WAVES + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool live = t < T;  // dead rows still run the DPP steps (they read only their own row)
+    const float *l = logits + (size_t)(live ? t : 0) * E;
+    uint32_t khi[PER];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < ROUTE_MAX_PER_LANE; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E) {
-            lg[j] = l[e];
-            sc[j] = bias ? lg[j] + bias[e] : lg[j];
-            mx = fmaxf(mx, lg[j]);
-        } else {
-            lg[j] = 0.0f;
-            sc[j] = -INFINITY;
+    for (int j = 0; j < PER; ++j) {
+        const int e = l16 + 16 * j;
+        khi[j] = 0;
+        if (e < E && live) {
+            const float lg = l[e];
+            mx = fmaxf(mx, lg);
+            khi[j] = order_key(bias ? lg + bias[e] : lg);
         }
     }
-    mx = group_max<64>(mx);
-    uint32_t taken = 0;  // bit j: expert lane+64j already picked
-    float my_ex = 0.0f;  // lane k keeps the k-th pick's exp
+    mx = fmax_step<DPP_QUAD_XOR1>(mx);
+    mx = fmax_step<DPP_QUAD_XOR2>(mx);
+    mx = fmax_step<DPP_HALF_MIRROR>(mx);
+    mx = fmax_step<DPP_MIRROR>(mx);
+
     int my_idx = 0;
+    uint32_t taken = 0;  // bit j: slot j already picked (a mask, not a dynamic register index)
+#pragma unroll 1
     for (int k = 0; k < K; ++k) {
-        float bs = -INFINITY;
-        int bi = 0x7fffffff;
+        // lane-local best untaken key (slots ascend in expert id: strict '>' keeps the lower id)
+        uint32_t hi = 0;
+        int jbest = 0;
 #pragma unroll
-        for (int j = 0; j < ROUTE_MAX_PER_LANE; ++j) {
-            const int e = lane + 64 * j;
-            if (e < E && !(taken & (1u << j)) && (sc[j] > bs || bi == 0x7fffffff)) {
-                bs = sc[j];
-                bi = e;
-            }
+        for (int j = 0; j < PER; ++j) {
+            const bool gt = !((taken >> j) & 1u) && khi[j] > hi;
+            hi = gt ? khi[j] : hi;
+            jbest = gt ? j : jbest;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float os = __shfl_xor(bs, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (oi != 0x7fffffff && (bi == 0x7fffffff || os > bs || (os == bs && oi < bi))) {
-                bs = os;
-                bi = oi;
-            }
-        }
-        // owner lane marks it taken and evaluates the exponent
-        float ex = 0.0f;
-        if ((bi & 63) == lane) {
-            const int j = bi >> 6;
-#pragma unroll
-            for (int jj = 0; jj < ROUTE_MAX_PER_LANE; ++jj)
-                if (jj == j) {
-                    taken |= 1u << jj;
-                    ex = expf(lg[jj] - mx);
-                }
-        }
-        ex = __shfl(ex, bi & 63, 64);
-        if (lane == k) {
-            my_ex = ex;
-            my_idx = bi;
-        }
+        uint32_t lo = hi ? ~(uint32_t)(l16 + 16 * jbest) : 0u;
+        key_max_step<DPP_QUAD_XOR1>(hi, lo);
+        key_max_step<DPP_QUAD_XOR2>(hi, lo);
+        key_max_step<DPP_HALF_MIRROR>(hi, lo);
+        key_max_step<DPP_MIRROR>(hi, lo);
+        const int best = (int)~lo;
+        if ((best & 15) == l16)
+            taken |= 1u << (best >> 4);
+        if (l16 == k)
+            my_idx = best;
     }
-    // sum of the K exponents in pick order
+    float my_ex = 0.0f;
+    if (l16 < K && live)
+        my_ex = expf(l[my_idx] - mx);
     float denom = 0.0f;
     for (int k = 0; k < K; ++k)
-        denom += __shfl(my_ex, k, 64);
-    if (lane < K) {
-        topk_idx[(size_t)t * K + lane] = my_idx;
-        topk_w[(size_t)t * K + lane] = my_ex / denom;
+        denom += __shfl(my_ex, (lane & 48) | k, 64);
+    if (l16 < K && live) {
+        topk_idx[(size_t)t * K + l16] = my_idx;
+        topk_w[(size_t)t * K + l16] = my_ex / denom;
     }
 }
 
@@ -93,9 +118,24 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
 {
     if (T == 0)
         return hipSuccess;
-    const int grid = (T + ROUTE_WAVES - 1) / ROUTE_WAVES;
-    hipLaunchKernelGGL(route_kernel, dim3(grid), dim3(ROUTE_WAVES * 64), 0, s, logits, bias, T, E, K, topk_idx,
-                       topk_w);
+    if (E > 16 * ROUTE_MAX_PER_LANE || K > 16)
+        return hipErrorInvalidValue;
+    const int tokens_per_block = ROUTE_WAVES * 4;
+    const int grid = (T + tokens_per_block - 1) / tokens_per_block;
+    const dim3 g(grid), b(ROUTE_WAVES * 64);
+    const int per = (E + 15) >> 4;
+    if (per <= 1)
+        hipLaunchKernelGGL(route_kernel<1>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+    else if (per <= 2)
+        hipLaunchKernelGGL(route_kernel<2>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+    else if (per <= 4)
+        hipLaunchKernelGGL(route_kernel<4>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+    else if (per <= 8)
+        hipLaunchKernelGGL(route_kernel<8>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+    else if (per <= 16)
+        hipLaunchKernelGGL(route_kernel<16>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+    else
+        hipLaunchKernelGGL(route_kernel<32>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
     return hipGetLastError();
 }
 
