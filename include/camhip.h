@@ -147,6 +147,48 @@ CAMHIP_API camhipStatus camhipMoeCombineNormalGetWorkspaceSize(
 CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                void *stream);
 
+/* ------------------------------------------------------------------ grouped expert GEMMs
+ * The GMM1 / SwiGLU / GMM2 stages of fused_deep_moe as standalone calls
+ * (fused_deep_moe.h:56-238; kernels
+ * grouped_matmul_slice_m_per_token_dequant_swiglu_quant_multistage_workspace.h:299-455 and
+ * grouped_matmul_slice_m_per_token_dequant_multistage_workspace.h:141-292).  The
+ * reference computes them in int8 only; these take bf16, or fp8 e4m3fn with
+ * DeepSeek-style block scales.
+ * x [m, k]: rows in dispatch order; expert g owns groupList[g] consecutive
+ * rows starting at the sum of the earlier counts (groupList is int64 on the
+ * device, as recvTokensPerExpert / expert_token_nums).  Rows past the sum are
+ * neither read for output nor written.
+ * weight [numGroups, n, k] with k contiguous (the transpose of the reference's
+ * logical [L, k, n] layout).  dtype: CAMHIP_DTYPE_BF16 or CAMHIP_DTYPE_FP8;
+ * for fp8, xScale [m, k/128] and weightScale [numGroups, n/128, k/128] fp32
+ * (dequantised value = code * scale).  Accumulation is fp32. */
+#define CAMHIP_DTYPE_BF16 0
+#define CAMHIP_DTYPE_FP8 3
+
+/* GMM1 + SwiGLU: n = 2I, weight rows [0,I) gate, [I,2I) up;
+ * h[m, I] = silu(x W_gate^T) * (x W_up^T), silu(g) = g / (1 + exp(-g))
+ * (block_epilogue_per_token_dequant_swiglu.h:256-286).
+ * outQuant CAMHIP_QUANT_NONE: h bf16; CAMHIP_QUANT_FP8_BLOCK: h fp8 e4m3fn with
+ * hScale [m, I/128], quantised per 1x128 block like the dispatch quantiser.
+ * Limits: 1 <= numGroups <= 512, k a multiple of 64 (bf16) / 128 (fp8),
+ * I a multiple of 128, m*k and n*k bytes below 4 GiB. */
+CAMHIP_API camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(
+    const void *x, const float *xScale, const int64_t *groupList, int64_t numGroups, int64_t m, int64_t k, int64_t n,
+    const void *weight, const float *weightScale, int64_t dtype, int64_t outQuant, void *h, float *hScale,
+    uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                                  void *stream);
+
+/* GMM2: out[m, n] = bf16(x W^T) per group (block_epilogue_per_token_dequant.hpp:338-361).
+ * Limits as above, with n a multiple of 256. */
+CAMHIP_API camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const float *xScale,
+                                                            const int64_t *groupList, int64_t numGroups, int64_t m,
+                                                            int64_t k, int64_t n, const void *weight,
+                                                            const float *weightScale, int64_t dtype, uint16_t *out,
+                                                            uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,166 @@
+"""GPU parity of the grouped expert GEMMs (G1 GMM1+SwiGLU, G3 GMM2) against
+the CPU oracle at small ragged shapes and against a torch fp32 reference on
+the GPU at larger shapes.
+
+Tolerances: bf16 within 2e-2 relative, fp8 within 5e-2
+relative, measured as max|got - ref| / max|ref| per output tensor.  The
+reference's own fused-vs-small-op check is allclose(rtol=0.02, atol=2.0) on a
+fraction of elements (test_fused_deep_moe.py:443, util/tool.py:47-65); the
+max-norm bound used here is stricter.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import umdk_amd  # noqa: F401
+    return torch.ops.umdk_cam_op_lib
+
+
+def relerr(got, ref):
+    got = torch.as_tensor(got, dtype=torch.float64)
+    ref = torch.as_tensor(ref, dtype=torch.float64)
+    return ((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def b16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def fp8_quant_rows(x):
+    """DeepSeek 1x128 quantiser (the same recipe as the dispatch kernel)."""
+    m, k = x.shape
+    xv = x.float().view(m, k // 128, 128)
+    amax = xv.abs().amax(2).clamp(min=1e-4)
+    q = (xv * torch.div(torch.full_like(amax, 448.0), amax).unsqueeze(2)).to(torch.float8_e4m3fn)
+    return q.view(m, k), torch.div(amax, torch.full_like(amax, 448.0))
+
+
+def fp8_quant_weight(w):
+    """128x128 block quantisation of [L, n, k] weights."""
+    L, n, k = w.shape
+    wv = w.float().view(L, n // 128, 128, k // 128, 128)
+    amax = wv.abs().amax(dim=(2, 4)).clamp(min=1e-6)
+    q = (wv / (amax / 448.0)[:, :, None, :, None]).to(torch.float8_e4m3fn)
+    return q.view(L, n, k), (amax / 448.0).contiguous()
+
+
+def dq_rows(q, s):
+    m, k = q.shape
+    return (q.float().view(m, k // 128, 128) * s.float().view(m, k // 128, 1)).view(m, k)
+
+
+SMALL = [([5, 0, 300], 256, 256), ([1], 128 * 4, 128), ([17, 256, 255, 1, 0, 9], 512, 128)]
+
+
+@pytest.mark.parametrize("counts,H,I", SMALL)
+def test_gmm_bf16_matches_oracle(ops, counts, H, I):
+    print(f"gmm bf16 counts={counts} H={H} I={I}", flush=True)
+    g = torch.Generator().manual_seed(sum(counts) + H)
+    L, M = len(counts), sum(counts)
+    x = torch.randn(M + 3, H, generator=g).bfloat16()            # 3 spare rows past the groups
+    w1 = (torch.randn(L, 2 * I, H, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(L, H, I, generator=g) * 0.05).bfloat16()
+    gl = torch.tensor(counts, dtype=torch.int64)
+    h, _ = ops.grouped_matmul_swiglu(x.cuda(), None, gl.cuda(), w1.cuda(), None, 0)
+    rh = orc.gmm1_swiglu_bf16(b16(x), gl.numpy(), b16(w1))
+    hf = h.cpu().float()[:M]
+    assert relerr(hf, orc.bf16_to_f32(rh)[:M]) < 2e-2
+    hin = torch.randn(M + 3, I, generator=g).bfloat16()
+    out = ops.grouped_matmul(hin.cuda(), None, gl.cuda(), w2.cuda(), None)
+    ro = orc.gmm2_bf16(b16(hin), gl.numpy(), b16(w2))
+    assert relerr(out.cpu().float()[:M], orc.bf16_to_f32(ro)[:M]) < 2e-2
+
+
+@pytest.mark.parametrize("counts,H,I", SMALL)
+def test_gmm_fp8_matches_oracle(ops, counts, H, I):
+    print(f"gmm fp8 counts={counts} H={H} I={I}", flush=True)
+    g = torch.Generator().manual_seed(7 + sum(counts))
+    L, M = len(counts), sum(counts)
+    x = torch.randn(M + 3, H, generator=g)
+    xq, xs = fp8_quant_rows(x)
+    w1q, w1s = fp8_quant_weight(torch.randn(L, 2 * I, H, generator=g) * 0.05)
+    w2q, w2s = fp8_quant_weight(torch.randn(L, H, I, generator=g) * 0.05)
+    gl = torch.tensor(counts, dtype=torch.int64)
+    h, hs = ops.grouped_matmul_swiglu(xq.cuda(), xs.cuda(), gl.cuda(), w1q.cuda(), w1s.cuda(), 3)
+    u8 = lambda t: t.cpu().contiguous().view(torch.uint8).numpy()
+    rhq, rhs = orc.gmm1_swiglu_fp8(u8(xq), xs.numpy(), gl.numpy(), u8(w1q), w1s.numpy())
+    got_h = dq_rows(h.cpu(), hs.cpu())[:M]
+    ref_h = dq_rows(torch.from_numpy(rhq).view(torch.float8_e4m3fn), torch.from_numpy(rhs))[:M]
+    assert relerr(got_h, ref_h) < 5e-2
+    # GMM2 on the oracle's own h so that both sides multiply identical codes
+    out = ops.grouped_matmul(torch.from_numpy(rhq).view(torch.float8_e4m3fn).cuda(), torch.from_numpy(rhs).cuda(),
+                             gl.cuda(), w2q.cuda(), w2s.cuda())
+    ro = orc.gmm2_fp8(rhq, rhs, gl.numpy(), u8(w2q), w2s.numpy())
+    assert relerr(out.cpu().float()[:M], orc.bf16_to_f32(ro)[:M]) < 5e-2
+
+
+def _torch_ffn(x, counts, w1, w2, I):
+    hs, outs, off = [], [], 0
+    for e, c in enumerate(counts):
+        a = x[off:off + c].float()
+        gu = a @ w1[e].float().T
+        gg, uu = gu[:, :I], gu[:, I:]
+        h = (gg / (1 + torch.exp(-gg)) * uu)
+        hs.append(h)
+        outs.append(h.bfloat16().float() @ w2[e].float().T)
+        off += c
+    return torch.cat(hs), torch.cat(outs)
+
+
+def test_gmm_bf16_mixtral_like_vs_torch(ops):
+    # Mixtral-shaped slice: 8 experts, H=4096, I=1792 (an eighth of 14336), skewed counts
+    counts = [900, 37, 2048, 0, 511, 1300, 256, 1]
+    H, I = 4096, 1792
+    g = torch.Generator(device="cuda").manual_seed(3)
+    M = sum(counts)
+    x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
+    w1 = (torch.randn(8, 2 * I, H, device="cuda", generator=g) * 0.02).bfloat16()
+    w2 = (torch.randn(8, H, I, device="cuda", generator=g) * 0.02).bfloat16()
+    gl = torch.tensor(counts, dtype=torch.int64, device="cuda")
+    h, _ = ops.grouped_matmul_swiglu(x, None, gl, w1, None, 0)
+    out = ops.grouped_matmul(h, None, gl, w2, None)
+    rh, ro = _torch_ffn(x, counts, w1, w2, I)
+    assert relerr(h.float(), rh) < 2e-2
+    assert relerr(out.float(), ro) < 2e-2
+
+
+def test_gmm_fp8_dsv3_like_vs_torch(ops):
+    # DeepSeek-V3 expert shapes (H=7168, I=2048) on 6 experts with Zipf-like counts
+    counts = [1500, 700, 300, 129, 64, 3]
+    H, I = 7168, 2048
+    g = torch.Generator(device="cuda").manual_seed(5)
+    M = sum(counts)
+    x = torch.randn(M, H, device="cuda", generator=g)
+    xq, xs = fp8_quant_rows(x)
+    w1q, w1s = fp8_quant_weight(torch.randn(6, 2 * I, H, device="cuda", generator=g) * 0.02)
+    w2q, w2s = fp8_quant_weight(torch.randn(6, H, I, device="cuda", generator=g) * 0.02)
+    gl = torch.tensor(counts, dtype=torch.int64, device="cuda")
+    h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1q, w1s, 3)
+    out = ops.grouped_matmul(h, hs, gl, w2q, w2s)
+    # fp32 reference on the dequantised operands
+    xd = dq_rows(xq, xs)
+    w1d = (w1q.float().view(6, 2 * I // 128, 128, H // 128, 128) * w1s[:, :, None, :, None]).view(6, 2 * I, H)
+    w2d = (w2q.float().view(6, H // 128, 128, I // 128, 128) * w2s[:, :, None, :, None]).view(6, H, I)
+    rh, _ = _torch_ffn(xd, counts, w1d, w2d, I)
+    assert relerr(dq_rows(h, hs), rh) < 5e-2
+    ro, off = [], 0
+    hd = dq_rows(h, hs)
+    for e, c in enumerate(counts):
+        ro.append(hd[off:off + c] @ w2d[e].T)
+        off += c
+    assert relerr(out.float(), torch.cat(ro)) < 5e-2
+
+
+def test_gmm_rejects_bad_shapes(ops):
+    x = torch.zeros(8, 100, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(1, 256, 100, dtype=torch.bfloat16, device="cuda")
+    gl = torch.tensor([8], dtype=torch.int64, device="cuda")
+    with pytest.raises(Exception, match="multiple of"):
+        ops.grouped_matmul(x, None, gl, w, None)

@@ -24,6 +24,8 @@ SIGNATURES = {
     "camhipNotifyDispatch": "p iiii pppppp",
     "camhipMoeDispatchNormal": "pppppp iiiiiiii ppp",
     "camhipMoeCombineNormal": "pp i pp iiiiii p",
+    "camhipGroupedMatmulSwiglu": "ppp iiii pp ii pp",
+    "camhipGroupedMatmul": "ppp iiii pp i p",
 }
 
 _lib = None

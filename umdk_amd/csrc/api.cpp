@@ -12,6 +12,7 @@
 #include <string>
 
 #include "../../include/camhip.h"
+#include "gmm.h"
 #include "launchers.h"
 
 struct camhipExecutor {
@@ -293,6 +294,87 @@ camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const
 camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
 {
     return run_executor("moe_combine", workspace, workspaceSize, executor, stream);
+}
+
+// ---------------------------------------------------------------- grouped GEMMs
+static camhipStatus check_gmm(const char *op, const void *x, const float *xScale, const int64_t *groupList,
+                              int64_t numGroups, int64_t m, int64_t k, int64_t n, const void *weight,
+                              const float *weightScale, int64_t dtype, bool swiglu)
+{
+    CHECK_PARAM(dtype == CAMHIP_DTYPE_BF16 || dtype == CAMHIP_DTYPE_FP8, "%s: dtype %lld not supported (0 or 3)", op,
+                (long long)dtype);
+    CHECK_PARAM(numGroups >= 1 && numGroups <= 512, "%s: numGroups %lld out of [1,512]", op, (long long)numGroups);
+    CHECK_PARAM(m >= 1 && m <= (1 << 24), "%s: m %lld out of range", op, (long long)m);
+    const int64_t esz = dtype == CAMHIP_DTYPE_FP8 ? 1 : 2;
+    CHECK_PARAM(k >= 128 / esz && (k * esz) % 128 == 0, "%s: k %lld must be a multiple of %lld", op, (long long)k,
+                (long long)(128 / esz));
+    if (swiglu)
+        CHECK_PARAM(n >= 256 && n % 256 == 0, "%s: n = 2I = %lld needs I a multiple of 128", op, (long long)n);
+    else
+        CHECK_PARAM(n >= 256 && n % 256 == 0, "%s: n %lld must be a multiple of 256", op, (long long)n);
+    CHECK_PARAM(m * k * esz < (int64_t)1 << 32 && n * k * esz < (int64_t)1 << 32,
+                "%s: x or one group's weight exceeds 4 GiB", op);
+    CHECK_PTR(x);
+    CHECK_PTR(groupList);
+    CHECK_PTR(weight);
+    if (dtype == CAMHIP_DTYPE_FP8) {
+        CHECK_PTR(xScale);
+        CHECK_PTR(weightScale);
+    }
+    return CAMHIP_SUCCESS;
+}
+
+camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(const void *x, const float *xScale, const int64_t *groupList,
+                                                       int64_t numGroups, int64_t m, int64_t k, int64_t n,
+                                                       const void *weight, const float *weightScale, int64_t dtype,
+                                                       int64_t outQuant, void *h, float *hScale,
+                                                       uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    camhipStatus st = check_gmm("grouped_matmul_swiglu", x, xScale, groupList, numGroups, m, k, n, weight,
+                                weightScale, dtype, true);
+    if (st != CAMHIP_SUCCESS)
+        return st;
+    CHECK_PARAM(outQuant == CAMHIP_QUANT_NONE || outQuant == CAMHIP_QUANT_FP8_BLOCK,
+                "grouped_matmul_swiglu: outQuant %lld not supported (0 or 3)", (long long)outQuant);
+    CHECK_PTR(h);
+    if (outQuant == CAMHIP_QUANT_FP8_BLOCK)
+        CHECK_PTR(hScale);
+    cam::GmmArgs a{(const uint8_t *)x, xScale, groupList, (int)numGroups, (int)m, (int)k, (int)n,
+                   (const uint8_t *)weight, weightScale, (uint8_t *)h, hScale};
+    const int dt = (int)dtype;
+    const int epi = outQuant == CAMHIP_QUANT_FP8_BLOCK ? cam::EPI_SWIGLU_FP8 : cam::EPI_SWIGLU_BF16;
+    if (dt == cam::DT_BF16 && epi == cam::EPI_SWIGLU_FP8)
+        return fail(CAMHIP_ERROR_INVALID_PARAM, "grouped_matmul_swiglu: fp8 h needs fp8 inputs");
+    return make_executor(
+        0, [=](void *, hipStream_t s) { return cam::launch_gmm(a, dt, epi, s); }, workspaceSize, executor);
+}
+
+camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return run_executor("grouped_matmul_swiglu", workspace, workspaceSize, executor, stream);
+}
+
+camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const float *xScale, const int64_t *groupList,
+                                                 int64_t numGroups, int64_t m, int64_t k, int64_t n,
+                                                 const void *weight, const float *weightScale, int64_t dtype,
+                                                 uint16_t *out, uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    camhipStatus st = check_gmm("grouped_matmul", x, xScale, groupList, numGroups, m, k, n, weight, weightScale,
+                                dtype, false);
+    if (st != CAMHIP_SUCCESS)
+        return st;
+    CHECK_PTR(out);
+    cam::GmmArgs a{(const uint8_t *)x, xScale, groupList, (int)numGroups, (int)m, (int)k, (int)n,
+                   (const uint8_t *)weight, weightScale, (uint8_t *)out, nullptr};
+    const int dt = (int)dtype;
+    return make_executor(
+        0, [=](void *, hipStream_t s) { return cam::launch_gmm(a, dt, cam::EPI_PLAIN, s); }, workspaceSize,
+        executor);
+}
+
+camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return run_executor("grouped_matmul", workspace, workspaceSize, executor, stream);
 }
 
 }  // extern "C"

@@ -34,6 +34,10 @@ _def.define(
     "moe_combine_prefill(Tensor x, Tensor topk_idx, Tensor topk_weights, Tensor src_idx, Tensor send_head, "
     "str group_ep, int rank, int num_ranks) -> Tensor")
 _def.define("moe_route(Tensor logits, Tensor? bias, int topk) -> (Tensor, Tensor)")
+_def.define("grouped_matmul_swiglu(Tensor x, Tensor? x_scale, Tensor group_list, Tensor weight, "
+            "Tensor? weight_scale, int out_quant=0) -> (Tensor, Tensor)")
+_def.define("grouped_matmul(Tensor x, Tensor? x_scale, Tensor group_list, Tensor weight, Tensor? weight_scale) "
+            "-> Tensor")
 
 _impl = torch.library.Library(LIB_NAME, "IMPL", "CUDA")
 
@@ -178,6 +182,70 @@ def moe_route(logits, bias, topk):
     return idx, w
 
 
+def _gmm_common(x, x_scale, group_list, weight, weight_scale, op):
+    _check(x.dim() == 2 and x.is_contiguous(), f"{op}: x must be 2-D and contiguous")
+    _check(weight.dim() == 3 and weight.is_contiguous(), f"{op}: weight must be [groups, n, k] contiguous")
+    _check(group_list.dtype == torch.int64 and group_list.dim() == 1, f"{op}: group_list must be 1-D int64")
+    L, n, k = weight.shape
+    _check(group_list.numel() == L, f"{op}: group_list has {group_list.numel()} groups, weight {L}")
+    _check(x.shape[1] == k, f"{op}: x has {x.shape[1]} columns, weight k = {k}")
+    if x.dtype == torch.bfloat16:
+        _check(weight.dtype == torch.bfloat16, f"{op}: bf16 x needs bf16 weight")
+        dt = 0
+    else:
+        _check(x.dtype == torch.float8_e4m3fn and weight.dtype == torch.float8_e4m3fn,
+               f"{op}: x and weight must both be bfloat16 or both float8_e4m3fn")
+        _check(x_scale is not None and weight_scale is not None, f"{op}: fp8 needs x_scale and weight_scale")
+        _check(x_scale.dtype == torch.float32 and tuple(x_scale.shape) == (x.shape[0], k // 128),
+               f"{op}: x_scale must be float32 [m, k/128]")
+        _check(weight_scale.dtype == torch.float32 and tuple(weight_scale.shape) == (L, n // 128, k // 128),
+               f"{op}: weight_scale must be float32 [groups, n/128, k/128]")
+        dt = 3
+    return dt, L, n, k
+
+
+def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quant=0):
+    """GMM1 + SwiGLU over ragged expert groups (addition; the reference runs
+    this stage inside fused_deep_moe, grouped_matmul_slice_m_per_token_dequant_
+    swiglu_quant_multistage_workspace.h:299-455).  weight [L, 2I, k]: rows
+    [0,I) gate, [I,2I) up.  Returns (h [m, I], h_scale): bf16 h and an empty
+    scale for out_quant=0; fp8 h and [m, I/128] scales for out_quant=3."""
+    dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul_swiglu")
+    m = x.shape[0]
+    I = n // 2
+    if out_quant == QUANT_FP8_BLOCK:
+        h = torch.empty((m, I), dtype=torch.float8_e4m3fn, device=x.device)
+        hs = torch.empty((m, I // 128), dtype=torch.float32, device=x.device)
+    else:
+        _check(out_quant == QUANT_NONE, "grouped_matmul_swiglu: out_quant must be 0 or 3")
+        h = torch.empty((m, I), dtype=torch.bfloat16, device=x.device)
+        hs = torch.empty(0, dtype=torch.float32, device=x.device)
+    _lib.call("camhipGroupedMatmulSwiglu", _lib.ptr(x), _lib.ptr(x_scale), _lib.ptr(group_list), L, m, k, n,
+              _lib.ptr(weight), _lib.ptr(weight_scale), dt, out_quant, _lib.ptr(h),
+              _lib.ptr(hs) if out_quant else None, device=x.device)
+    return h, hs
+
+
+def grouped_matmul(x, x_scale, group_list, weight, weight_scale):
+    """GMM2 over ragged expert groups: out[m, n] = bf16(x W^T) (addition; the
+    reference's grouped_matmul_slice_m_per_token_dequant_multistage_workspace.h:141-292)."""
+    dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul")
+    m = x.shape[0]
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _lib.call("camhipGroupedMatmul", _lib.ptr(x), _lib.ptr(x_scale), _lib.ptr(group_list), L, m, k, n,
+              _lib.ptr(weight), _lib.ptr(weight_scale), dt, _lib.ptr(out), device=x.device)
+    return out
+
+
+def prepack_weight(w_lkn):
+    """Reference logical layout [L, k, n] (e.g. W1 [L, H, 2I], API guide
+    doc/en/cam/CAM API Guide.md:183-186) -> the [L, n, k] k-contiguous layout
+    the grouped GEMMs read.  A one-time copy at weight load."""
+    return w_lkn.transpose(1, 2).contiguous()
+
+
+_impl.impl("grouped_matmul_swiglu", grouped_matmul_swiglu)
+_impl.impl("grouped_matmul", grouped_matmul)
 _impl.impl("get_dispatch_layout", get_dispatch_layout)
 _impl.impl("moe_dispatch_prefill", moe_dispatch_prefill)
 _impl.impl("moe_combine_prefill", moe_combine_prefill)
