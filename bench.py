@@ -62,6 +62,134 @@ def cpu_baseline(T, H, E, K, seed):
                       f"{dt * 1e3:.0f} ms/step"}
 
 
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def zipf_bias(E, s, seed):
+    """log-popularity bias: expert popularity ~ 1/rank^s over a seeded permutation of the ids"""
+    g = torch.Generator().manual_seed(seed + 17)
+    rank = torch.empty(E)
+    rank[torch.randperm(E, generator=g)] = torch.arange(1, E + 1, dtype=torch.float32)
+    return -s * torch.log(rank)
+
+
+def make_weights(L, H, I, dtype, dev, seed):
+    """W1 [L, 2I, H], W2 [L, H, I] ~ N(0, 0.02); fp8: 128x128 block-quantised e4m3fn + fp32 scales."""
+    g = torch.Generator(device=dev).manual_seed(seed + 5)
+
+    def one(shape):
+        w = torch.randn(shape, device=dev, generator=g, dtype=torch.float32) * 0.02
+        if dtype == "bf16":
+            return w.bfloat16(), None
+        Ln, n, k = shape
+        wv = w.view(Ln, n // 128, 128, k // 128, 128)
+        amax = wv.abs().amax(dim=(2, 4)).clamp(min=1e-6)
+        sc = amax / 448.0
+        q = (wv / sc[:, :, None, :, None]).to(torch.float8_e4m3fn).view(Ln, n, k)
+        del wv, w
+        return q, sc.contiguous()
+
+    w1, s1 = one((L, 2 * I, H))
+    w2, s2 = one((L, H, I))
+    return w1, s1, w2, s2
+
+
+def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
+    """Full layer (route, layout, dispatch, GMM1+SwiGLU, GMM2, combine) on one rank's L local experts."""
+    from umdk_amd.plan import MoeLayerPlan
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).bfloat16().to(dev)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    bias = zipf_bias(E, 1.1, seed).to(dev) if bias_kind == "zipf" else None
+    w1, s1, w2, s2 = make_weights(L, H, I, dtype, dev, seed)
+    plan = MoeLayerPlan(T, H, E, K, L, I, dtype=dtype, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+
+    def step(i=None):
+        plan.route(logits, bias)
+        plan.layout()
+        plan.dispatch(x)
+        if i is not None:
+            ev[i][0].record(stream)
+        plan.gmm1(w1, s1)
+        if i is not None:
+            ev[i][1].record(stream)
+        plan.gmm2(w2, s2)
+        if i is not None:
+            ev[i][2].record(stream)
+        plan.combine(plan.y)
+        if i is not None:
+            ev[i][3].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    g1 = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    g2 = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    counts = plan.recv_tokens_per_expert[:L].cpu()
+    M = int(counts.sum())
+    touched = int((counts > 0).sum())
+    esz = 1 if dtype == "fp8" else 2
+    f1, f2 = 2.0 * M * H * 2 * I, 2.0 * M * I * H
+    wb1, wb2 = touched * 2 * I * H * esz, touched * H * I * esz
+    peak = FP8_PEAK_TFLOPS if dtype == "fp8" else BF16_PEAK_TFLOPS
+    # roofline time per GEMM: max(FLOP/peak, weight+activation bytes/HBM peak)
+    ab1 = M * H * esz + M * I * esz + wb1
+    ab2 = M * I * esz + M * H * 2 + wb2
+    roof = max(f1 / (peak * 1e12), ab1 / (HBM_PEAK_GBPS * 1e9)) + max(f2 / (peak * 1e12), ab2 / (HBM_PEAK_GBPS * 1e9))
+    tflops = (f1 + f2) / ((g1 + g2) * 1e-3) / 1e12
+    del w1, w2
+    return {"workload": name, "tokens": T, "hidden": H, "experts_routed": E, "local_experts": L, "topk": K,
+            "intermediate": I, "dtype": dtype, "local_rows_M": M, "experts_touched": touched,
+            "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
+            "gmm1_ms": g1, "gmm2_ms": g2, "gemm_tflops": tflops, "gemm_frac_of_mfma_peak": tflops / peak,
+            "gemm_roofline_frac": roof / ((g1 + g2) * 1e-3),
+            "gemm_bound": "mfma" if (f1 + f2) / (peak * 1e12) > (ab1 + ab2) / (HBM_PEAK_GBPS * 1e9) else "hbm"}
+
+
+def gemm_sweep(steps, warmup, seed):
+    """fp8 GMM1+GMM2 at DeepSeek-V3 expert shapes (32 experts, H=7168, I=2048) for growing M."""
+    from umdk_amd import ops
+    dev = torch.device("cuda:0")
+    H, I, L = 7168, 2048, 32
+    w1, s1, w2, s2 = make_weights(L, H, I, "fp8", dev, seed)
+    out = []
+    for M in (4096, 8192, 16384, 32768, 65536):
+        gl = torch.full((L,), M // L, dtype=torch.int64, device=dev)
+        xq = (torch.randn(M, H, device=dev) * 0.5).to(torch.float8_e4m3fn)
+        xs = torch.full((M, H // 128), 0.01, device=dev)
+        for _ in range(warmup):
+            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, 3)
+            ops.grouped_matmul(h, hs, gl, w2, s2)
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        for _ in range(steps):
+            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, 3)
+        e[1].record()
+        for _ in range(steps):
+            ops.grouped_matmul(h, hs, gl, w2, s2)
+        e[2].record()
+        torch.cuda.synchronize()
+        t1 = e[0].elapsed_time(e[1]) / steps
+        t2 = e[1].elapsed_time(e[2]) / steps
+        f1, f2 = 2.0 * M * H * 2 * I, 2.0 * M * I * H
+        out.append({"M": M, "gmm1_ms": t1, "gmm1_tflops": f1 / t1 / 1e9, "gmm2_ms": t2, "gmm2_tflops": f2 / t2 / 1e9,
+                    "frac_of_fp8_peak": (f1 + f2) / (t1 + t2) / 1e9 / FP8_PEAK_TFLOPS})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -69,6 +197,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--config", default="2", choices=["2", "3", "4", "sweep", "all"],
+                    help="2: dispatch+combine headline (default; also reports configs 3 and 4 briefly); "
+                         "3/4: only that layer config; sweep: fp8 grouped-GEMM M-sweep")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
     args = ap.parse_args()
@@ -87,6 +218,16 @@ def main():
 
     import umdk_amd  # noqa: F401
     from umdk_amd.plan import MoePrefillPlan
+
+    cfg3 = lambda st, wu: run_layer("config3: Mixtral-8x7B grouped SwiGLU FFN, bf16", 8192, 4096, 8, 2, 8, 14336,
+                                    "bf16", st, wu, args.seed, None)
+    cfg4 = lambda st, wu: run_layer("config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), fp8",
+                                    4096, 7168, 256, 8, 32, 2048, "fp8", st, wu, args.seed, "zipf")
+    if args.config in ("3", "4", "sweep"):
+        r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
+             "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed)}[args.config]()
+        print(json.dumps({"config": args.config, "result": r}))
+        return
 
     T, H, E, K = 4096, 7168, 256, 8
     dev = torch.device("cuda:0")
@@ -157,6 +298,15 @@ def main():
         "dispatch_combine_GBps": dc_gbps,
         "dispatch_combine_frac": dc_gbps / HBM_PEAK_GBPS,
     }
+    del plan, x, y
+    torch.cuda.empty_cache()
+    if args.config in ("2", "all"):
+        result["config3"] = cfg3(10, 3)
+        torch.cuda.empty_cache()
+        result["config4"] = cfg4(20, 5)
+        torch.cuda.empty_cache()
+    if args.config == "all":
+        result["fp8_gemm_sweep"] = gemm_sweep(10, 3, args.seed)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(T, H, E, K, args.seed)
     print(json.dumps(result))

@@ -70,3 +70,66 @@ class MoePrefillPlan:
                     self.recv_count.data_ptr(), self.topk_w.data_ptr(), self.T, self.K, self.H, 1, 0, self.E,
                     self.out.data_ptr(), workspace=self.ws_combine, stream=stream, device=self.device)
         return self.out
+
+
+class MoeLayerPlan(MoePrefillPlan):
+    """Full expert layer on one EP rank: route over `E` experts, keep the
+    (t,k) pairs whose expert is one of this rank's `L` local experts (ids
+    0..L-1; the others would be sent to other ranks and are not routed here),
+    dispatch them, run GMM1+SwiGLU and GMM2 per local expert, and combine.
+
+    dtype "bf16": bf16 rows and weights, bf16 h.  dtype "fp8": fp8 e4m3fn rows
+    with 1x128 scales, fp8 weights with 128x128 scales, fp8 h with 1x128
+    scales; the output is bf16 either way.  Weights are [L, 2I, H] and
+    [L, H, I] with the reduction dimension contiguous.
+    """
+
+    def __init__(self, T, H, E, K, L, I, dtype="fp8", device="cuda"):
+        q = QUANT_FP8_BLOCK if dtype == "fp8" else QUANT_NONE
+        self.E_route = E
+        super().__init__(T, H, L, K, quant_mode=q, device=device)
+        self.L, self.I, self.dtype = L, I, dtype
+        dev = self.device
+        N = self.N
+        if dtype == "fp8":
+            self.h = torch.empty((N, I), dtype=torch.float8_e4m3fn, device=dev)
+            self.h_scale = torch.empty((N, I // 128), dtype=torch.float32, device=dev)
+        else:
+            self.h = torch.empty((N, I), dtype=torch.bfloat16, device=dev)
+            self.h_scale = None
+        self.y = torch.empty((N, H), dtype=torch.bfloat16, device=dev)
+        self.topk_idx = torch.empty((T, K), dtype=torch.int32, device=dev)
+
+    def route(self, logits, bias=None, stream=None):
+        _lib.launch("camhipMoeRoute", logits.data_ptr(), None if bias is None else bias.data_ptr(), self.T,
+                    self.E_route, self.K, self.topk_idx.data_ptr(), self.topk_w.data_ptr(), stream=stream,
+                    device=self.device)
+
+    def experts(self, w1, w1_scale, w2, w2_scale, stream=None):
+        self.gmm1(w1, w1_scale, stream)
+        return self.gmm2(w2, w2_scale, stream)
+
+    def gmm1(self, w1, w1_scale, stream=None):
+        dt = 3 if self.dtype == "fp8" else 0
+        xs = self.scales.data_ptr() if self.dtype == "fp8" else None
+        _lib.launch("camhipGroupedMatmulSwiglu", self.expand_x.data_ptr(), xs,
+                    self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.H, 2 * self.I, w1.data_ptr(),
+                    None if w1_scale is None else w1_scale.data_ptr(), dt, 3 if dt == 3 else 0, self.h.data_ptr(),
+                    None if self.h_scale is None else self.h_scale.data_ptr(), stream=stream, device=self.device)
+        return self.h
+
+    def gmm2(self, w2, w2_scale, stream=None):
+        dt = 3 if self.dtype == "fp8" else 0
+        _lib.launch("camhipGroupedMatmul", self.h.data_ptr(),
+                    None if self.h_scale is None else self.h_scale.data_ptr(),
+                    self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.I, self.H, w2.data_ptr(),
+                    None if w2_scale is None else w2_scale.data_ptr(), dt, self.y.data_ptr(), stream=stream,
+                    device=self.device)
+        return self.y
+
+    def forward(self, x, logits, bias, w1, w1_scale, w2, w2_scale, stream=None):
+        self.route(logits, bias, stream)
+        self.layout(stream)
+        self.dispatch(x, stream)
+        self.experts(w1, w1_scale, w2, w2_scale, stream)
+        return self.combine(self.y, stream)
