@@ -16,17 +16,21 @@
 //     (block_epilogue_per_token_dequant.hpp:338-361).
 //
 // Kernel design (gfx950):
-//   * 256 x 256 output tiles (for SwiGLU: 256 rows x 128 h-columns, i.e. 128
-//     gate + 128 up rows of W), 8 waves in a 2 x 4 grid, 128 x 64 per wave
-//     as 8 x 4 MFMA 16x16 tiles (v_mfma_f32_16x16x32_bf16, or
-//     v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales for fp8); the 128
-//     accumulators per lane leave room for the fp8 per-block rescale in VALU.
-//   * Each k-step moves 128 bytes of every A and W row (64 bf16 / 128 fp8)
-//     through LDS, double buffered, one barrier per k-step; global loads of
-//     the next k-step are in flight while the current one is multiplied.
-//     LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row & 7),
-//     so fragment reads spread over all banks.
-//   * MFMA operands are (W fragment, A fragment), so each lane's four
+//   * 128 x 256 output tiles (SwiGLU: 128 rows x 128 h-columns = 128 gate +
+//     128 up rows of W), 4 waves in a 2 x 2 grid, 64 x 128 per wave as 4 x 8
+//     MFMA 16x16 tiles: v_mfma_f32_16x16x32_bf16, or
+//     v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales for fp8.
+//   * Operands stream through a 3-stage LDS ring by direct global->LDS DMA
+//     (global_load_lds_dwordx4): no staging registers, and two k-steps of
+//     loads stay in flight while one is multiplied.  Each k-step is 128 bytes
+//     of every A and W row (64 bf16 / 128 fp8 elements); the fp8 activation
+//     scales of the k-step ride the same DMA (4-byte lanes).  A wave's loads
+//     are counted with s_waitcnt vmcnt and published with a bare s_barrier
+//     (no fence, so outstanding prefetches are not drained).
+//   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row & 7):
+//     each lane fetches the global chunk that belongs at its DMA slot, so
+//     fragment reads spread over all banks.
+//   * MFMA operands are (W fragment, A fragment), so a lane's four
 //     accumulators are four consecutive output columns of one row: the
 //     epilogue stores 8 contiguous bytes per lane without a transpose.
 //   * fp8: one MFMA of K=128 per (i,j) per k-step covers exactly one scale
@@ -42,10 +46,18 @@ namespace cam {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
-constexpr int GBM = 256, GBN = 256, GKB = 128;  // tile rows, tile W-rows, bytes per row per k-step
-constexpr int GTHREADS = 512;
+constexpr int GBM = 128, GBN = 256, GKB = 128;  // tile rows, tile W-rows, bytes per row per k-step
+constexpr int GTHREADS = 256;
+constexpr int GSTAGES = 3;
 constexpr int G_MAX_L = 512;
-constexpr int LDS_TILE = GBM * GKB;  // 32 KiB per operand per buffer
+constexpr int A_BYTES = GBM * GKB;           // 16 KiB
+constexpr int B_BYTES = GBN * GKB;           // 32 KiB
+constexpr int S_BYTES = 4 * 64 * 4;          // per-wave copies of 64 activation scales
+constexpr int STAGE_BYTES = A_BYTES + B_BYTES + S_BYTES;
+constexpr int A_LOADS = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage (1 KiB each)
+constexpr int B_LOADS = B_BYTES / 1024 / 4;
+
+constexpr int G_MAX_NK = 256;                // fp8 k <= 32768
 
 struct GroupTable {
     int tile_prefix[G_MAX_L + 1];  // exclusive prefix of M-tiles per expert
@@ -55,7 +67,6 @@ struct GroupTable {
 // Block-wide exclusive scans of ceil(cnt/GBM) and cnt over the L experts.
 __device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch)
 {
-    // scratch: 2 * GTHREADS ints
     const int tid = threadIdx.x;
     const int per = (L + GTHREADS - 1) / GTHREADS;
     int tsum = 0, rsum = 0;
@@ -99,33 +110,63 @@ __device__ void build_group_table(const int64_t *__restrict__ group_list, int L,
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * GKB + ((chunk ^ (row & 7)) << 4); }
 
+// s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima)
+template <int N> __device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
+// barrier without a memory fence: prefetches in flight stay in flight
+__device__ __forceinline__ void bar()
+{
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void dma16(const void *g, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
+}
+
 template <int DT, int EPI>
 __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t *lds_a = smem;                   // [2][GBM][GKB]
-    uint8_t *lds_b = smem + 2 * LDS_TILE;    // [2][GBN][GKB]
-    GroupTable *gt = reinterpret_cast<GroupTable *>(smem + 4 * LDS_TILE);
-    int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GTHREADS ints; reused for the fp8 amax exchange
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
+    int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GTHREADS ints: table scan, then the fp8 amax exchange
+    float *wsc = reinterpret_cast<float *>(scratch + 2 * GTHREADS);  // [2][G_MAX_NK] weight scales of the tile
 
     build_group_table(p.group_list, p.L, *gt, scratch);
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int wm = w >> 2, wn = w & 3;  // 2 row waves x 4 column waves
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w >> 1, wn = w & 1;
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
-    const int esz = DT == DT_FP8 ? 1 : 2;
-    const int kbytes = p.K * esz;  // bytes per row
-    const int nk = kbytes / GKB;
-    const int half_n = p.N / 2;    // I for SwiGLU
+    constexpr bool FP8 = DT == DT_FP8;
+    constexpr int LOADS = A_LOADS + B_LOADS + (FP8 ? 1 : 0);  // DMA instructions per wave per stage
+    const int esz = FP8 ? 1 : 2;
+    const uint32_t kbytes = (uint32_t)p.K * esz;  // bytes per row
+    const int nk = (int)(kbytes / GKB);
+    const int half_n = p.N / 2;                    // I for SwiGLU
     const int ntn = SWIGLU ? half_n / 128 : p.N / GBN;
-    const int total = gt->tile_prefix[p.L] * ntn;
+    const int total = __builtin_amdgcn_readfirstlane(gt->tile_prefix[p.L]) * ntn;
 
     // XCD-aware order: blocks b, b+8, b+16, ... run on the same XCD; give them consecutive tiles
     const int G = gridDim.x;
-    const int logical = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+    const int logical = (G & 7) ? (int)blockIdx.x : (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
 
-    for (int tile = (G & 7) ? (int)blockIdx.x : logical; tile < total; tile += G) {
+    // DMA slot of this lane inside a 1 KiB band (8 rows x 128 B): row l/8, physical chunk l%8,
+    // which holds logical chunk (l%8) ^ (l/8)
+    const int band_row = lane >> 3;
+    const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ band_row) << 4);
+
+    for (int tile = logical; tile < total; tile += G) {
         // ---- tile -> (expert, n-tile, m-tile)
         int lo = 0, hi = p.L - 1;
         while (lo < hi) {  // last e with tile_prefix[e]*ntn <= tile
@@ -135,158 +176,152 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
             else
                 hi = mid - 1;
         }
-        const int e = lo;
-        const int mt_e = gt->tile_prefix[e + 1] - gt->tile_prefix[e];
-        const int local = tile - gt->tile_prefix[e] * ntn;
+        // tile coordinates are block-uniform; say so, so that per-k-step weight-scale loads are
+        // scalar loads and do not share vmcnt with the DMA ring
+        const int e = __builtin_amdgcn_readfirstlane(lo);
+        const int mt_e = __builtin_amdgcn_readfirstlane(gt->tile_prefix[e + 1] - gt->tile_prefix[e]);
+        const int local = __builtin_amdgcn_readfirstlane(tile - gt->tile_prefix[e] * ntn);
         const int nt = local / mt_e, mt = local % mt_e;
-        const int seg0 = gt->row_off[e], seg1 = min(gt->row_off[e + 1], p.M);  // never write past row M
+        const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
+        const int seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
         const int row0 = seg0 + mt * GBM;
         const int n0 = SWIGLU ? nt * 128 : nt * GBN;  // first h-column (SwiGLU) or W row (plain)
 
-        // ---- byte offsets of this thread's 4 A chunks and 4 W chunks of k-step 0 (32-bit:
-        // the host checks that A and one expert's W are below 4 GiB)
-        uint32_t ga[4], gb[4];
+        // ---- per-lane byte offsets of the k-step-0 sources of this wave's DMA bands
         const uint8_t *wbase = p.W + (size_t)e * p.N * kbytes;
+        uint32_t ga[A_LOADS], gb[B_LOADS];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = (tid >> 3) + 64 * i, c = tid & 7;
-            const int arow = min(row0 + r, p.M - 1);
-            ga[i] = (uint32_t)arow * (uint32_t)kbytes + c * 16;
+        for (int i = 0; i < A_LOADS; ++i) {
+            const int r = (i * 4 + w) * 8 + band_row;  // tile row 0..127
+            ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off;
+        }
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) {
+            const int r = (i * 4 + w) * 8 + band_row;  // LDS W row 0..255
             int wrow;
             if (SWIGLU) {
-                // LDS row r belongs to column wave r/64: 32 gate rows then the 32 up rows
-                // of the same h-columns
-                const int wnn = r >> 6, jj = r & 63;
-                const int hcol = n0 + 32 * wnn + (jj & 31);
-                wrow = jj < 32 ? hcol : half_n + hcol;
+                // LDS rows [128 c, 128 c + 128) feed column wave c: 64 gate rows, then the
+                // 64 up rows of the same h-columns
+                const int c = r >> 7, jj = r & 127;
+                const int hcol = n0 + 64 * c + (jj & 63);
+                wrow = jj < 64 ? hcol : half_n + hcol;
             } else {
                 wrow = n0 + r;
             }
-            gb[i] = (uint32_t)wrow * (uint32_t)kbytes + c * 16;
+            gb[i] = (uint32_t)wrow * kbytes + chunk_off;
         }
+        // fp8: this wave's 64 activation-scale rows (rows of its row half wm)
+        const uint32_t gs = (uint32_t)min(row0 + wm * 64 + lane, p.M - 1) * (uint32_t)nk;
 
-        f32x4 acc[8][4];
+        auto issue = [&](int ks, int slot) {
+            const int kc = min(ks, nk - 1);  // past the end: reload the last k-step (keeps the count uniform)
+            uint8_t *st = smem + slot * STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < A_LOADS; ++i)
+                dma16(p.A + ga[i] + (uint32_t)kc * GKB, st + (i * 4 + w) * 1024);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < B_LOADS; ++i)
+                dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * 4 + w) * 1024);
+            if constexpr (FP8)
+                dma4(p.As + gs + kc, st + A_BYTES + B_BYTES + w * 256);
+        };
+
+        f32x4 acc[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
                 acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        u32x4 ra[4], rb[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ra[i] = *reinterpret_cast<const u32x4 *>(p.A + ga[i]);
-            rb[i] = *reinterpret_cast<const u32x4 *>(wbase + gb[i]);
-        }
-        __syncthreads();  // previous tile's readers are done with both buffers
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = (tid >> 3) + 64 * i, c = tid & 7;
-            *reinterpret_cast<u32x4 *>(lds_a + swz(r, c)) = ra[i];
-            *reinterpret_cast<u32x4 *>(lds_b + swz(r, c)) = rb[i];
-        }
-        __syncthreads();
-
-        // fp8 scale bookkeeping
-        const float *ws_g = nullptr, *ws_u = nullptr;
-        const int am0 = row0 + wm * 128 + l16;  // activation-scale row of fragment i: am0 + 16 i
-        if constexpr (DT == DT_FP8) {
+        if constexpr (FP8) {
+            // the tile's weight-scale rows (gate and up n-blocks, or the two 128-column halves)
+            // go to LDS once, so the k-loop issues no vector loads of its own
             const float *wsb = p.Ws + (size_t)e * (p.N / 128) * nk;
-            if (SWIGLU) {
-                ws_g = wsb + (size_t)(n0 / 128) * nk;
-                ws_u = wsb + (size_t)((half_n + n0) / 128) * nk;
-            } else {
-                ws_g = wsb + (size_t)((n0 + wn * 64) / 128) * nk;
+            const float *r0 = wsb + (size_t)((SWIGLU ? n0 : n0) / 128) * nk;
+            const float *r1 = wsb + (size_t)((SWIGLU ? half_n + n0 : n0 + 128) / 128) * nk;
+            for (int q = tid; q < nk; q += GTHREADS) {
+                wsc[q] = r0[q];
+                wsc[G_MAX_NK + q] = r1[q];
             }
+            __syncthreads();
         }
+        const float *ws_g = wsc + (SWIGLU ? 0 : wn * G_MAX_NK);
+        const float *ws_u = wsc + G_MAX_NK;
 
+        issue(0, 0);
+        issue(1, 1);
         for (int ks = 0; ks < nk; ++ks) {
-            const int cur = ks & 1;
-            const bool more = ks + 1 < nk;
-            if (more) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    ra[i] = *reinterpret_cast<const u32x4 *>(p.A + ga[i] + (uint32_t)(ks + 1) * GKB);
-                    rb[i] = *reinterpret_cast<const u32x4 *>(wbase + gb[i] + (uint32_t)(ks + 1) * GKB);
-                }
-            }
-            const uint8_t *la = lds_a + cur * LDS_TILE + (wm * 128) * GKB;
-            const uint8_t *lb = lds_b + cur * LDS_TILE + (wn * 64) * GKB;
+            const int cur = ks % GSTAGES;
+            wait_vmcnt<LOADS>();  // this wave's DMA for k-step ks has landed
+            bar();                // ... and every other wave's; slot (ks+2)%3 is free again
+            issue(ks + 2, (ks + 2) % GSTAGES);
+            const uint8_t *st = smem + cur * STAGE_BYTES;
+            const uint8_t *la = st + (wm * 64) * GKB;
+            const uint8_t *lb = st + A_BYTES + (wn * 128) * GKB;
             if constexpr (DT == DT_BF16) {
 #pragma unroll
                 for (int sub = 0; sub < 2; ++sub) {
-                    bf16x8 bfr[4];
+                    bf16x8 afr[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        bfr[j] = *reinterpret_cast<const bf16x8 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
+                    for (int i = 0; i < 4; ++i)
+                        afr[i] = *reinterpret_cast<const bf16x8 *>(la + swz(i * 16 + l16, sub * 4 + lg));
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const bf16x8 afr = *reinterpret_cast<const bf16x8 *>(la + swz(i * 16 + l16, sub * 4 + lg));
+                    for (int j = 0; j < 8; ++j) {
+                        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[j], afr, acc[i][j], 0, 0, 0);
+                        for (int i = 0; i < 4; ++i)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, afr[i], acc[i][j], 0, 0, 0);
                     }
                 }
             } else {
-                float sa[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    sa[i] = p.As[(uint32_t)min(am0 + 16 * i, p.M - 1) * (uint32_t)nk + ks];
+                const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * 256);
                 const float sg = ws_g[ks];
                 const float su = SWIGLU ? ws_u[ks] : sg;
-                i32x8 bfr[4];
+                float sa[4];
+                i32x8 afr[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg + 1));
-                    bfr[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                for (int i = 0; i < 4; ++i) {
+                    sa[i] = sst[i * 16 + l16];
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
+                    afr[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                    (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
-                    const i32x8 afr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                for (int j = 0; j < 8; ++j) {
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg + 1));
+                    const i32x8 bfr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                             (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    // in SwiGLU tiles a wave's columns j<4 are gate rows, j>=4 up rows
+                    const float sw = (SWIGLU && j >= 4) ? su : sg;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int i = 0; i < 4; ++i) {
                         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                        const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr[j], afr, z, 0, 0, 0,
-                                                                                         127, 0, 127);
-                        // in SwiGLU tiles a wave's columns j<2 are gate rows, j>=2 up rows
-                        const float s = sa[i] * ((SWIGLU && j >= 2) ? su : sg);
+                        const f32x4 d =
+                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr, afr[i], z, 0, 0, 0, 127, 0, 127);
+                        const float s = sa[i] * sw;
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
                             acc[i][j][q] += d[q] * s;
                     }
-                    // keep each fragment row's MFMA results short-lived (no hoisting of all 32)
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (more) {
-                uint8_t *na = lds_a + (cur ^ 1) * LDS_TILE;
-                uint8_t *nb = lds_b + (cur ^ 1) * LDS_TILE;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = (tid >> 3) + 64 * i, c = tid & 7;
-                    *reinterpret_cast<u32x4 *>(na + swz(r, c)) = ra[i];
-                    *reinterpret_cast<u32x4 *>(nb + swz(r, c)) = rb[i];
-                }
-            }
-            __syncthreads();
         }
+        wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
+        bar();
 
-        // ---- epilogue: lane holds rows m = row0 + wm*128 + 16 i + l16 and, per j, four
-        // consecutive columns 16 j + 4 lg + q of the wave's 64-wide column range
+        // ---- epilogue: lane holds rows m = row0 + wm*64 + 16 i + l16 and, per j, four
+        // consecutive columns 16 j + 4 lg + q of the wave's 128-wide column range
         if constexpr (EPI == EPI_PLAIN) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int m = row0 + wm * 128 + i * 16 + l16;
+            for (int i = 0; i < 4; ++i) {
+                const int m = row0 + wm * 64 + i * 16 + l16;
                 if (m >= seg1)
                     continue;
-                uint16_t *crow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * p.N + n0 + wn * 64 + 4 * lg;
+                uint16_t *crow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * p.N + n0 + wn * 128 + 4 * lg;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < 8; ++j) {
                     u32x2 v;
                     v[0] = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
                     v[1] = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
@@ -294,26 +329,26 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 }
             }
         } else {
-            // h-columns of this wave: n0 + 32 wn + 16 j + 4 lg + q, j < 2 (gate j, up j+2)
-            float h[8][2][4];
+            // h-columns of this wave: n0 + 64 wn + 16 j + 4 lg + q, j < 4 (gate j, up j+4)
+            float h[4][4][4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const float g = acc[i][j][q], u = acc[i][j + 2][q];
+                        const float g = acc[i][j][q], u = acc[i][j + 4][q];
                         h[i][j][q] = g / (1.0f + expf(-g)) * u;
                     }
             if constexpr (EPI == EPI_SWIGLU_BF16) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int m = row0 + wm * 128 + i * 16 + l16;
+                for (int i = 0; i < 4; ++i) {
+                    const int m = row0 + wm * 64 + i * 16 + l16;
                     if (m >= seg1)
                         continue;
-                    uint16_t *hrow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * half_n + n0 + 32 * wn + 4 * lg;
+                    uint16_t *hrow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * half_n + n0 + 64 * wn + 4 * lg;
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < 4; ++j) {
                         u32x2 v;
                         v[0] = f32_to_bf16(h[i][j][0]) | (f32_to_bf16(h[i][j][1]) << 16);
                         v[1] = f32_to_bf16(h[i][j][2]) | (f32_to_bf16(h[i][j][3]) << 16);
@@ -322,32 +357,32 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 }
             } else {
                 // fp8 1x128 requant: the tile's 128 h-columns of a row are one scale block,
-                // split over the four column waves; exchange partial amax through LDS
-                float *red = reinterpret_cast<float *>(scratch);  // [4][256]
+                // split over the two column waves; exchange partial amax through LDS
+                float *red = reinterpret_cast<float *>(scratch);  // [2][128]
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < 4; ++i) {
                     float mx = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
+                    for (int j = 0; j < 4; ++j)
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
                             mx = fmaxf(mx, fabsf(h[i][j][q]));
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                     if (lg == 0)
-                        red[wn * 256 + wm * 128 + i * 16 + l16] = mx;
+                        red[wn * 128 + wm * 64 + i * 16 + l16] = mx;
                 }
                 __syncthreads();
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int r = wm * 128 + i * 16 + l16;
+                for (int i = 0; i < 4; ++i) {
+                    const int r = wm * 64 + i * 16 + l16;
                     const int m = row0 + r;
-                    const float amax = fmaxf(fmaxf(fmaxf(red[r], red[256 + r]), fmaxf(red[512 + r], red[768 + r])), 1e-4f);
+                    const float amax = fmaxf(fmaxf(red[r], red[128 + r]), 1e-4f);
                     const float inv = 448.0f / amax;
                     if (m < seg1) {
-                        uint8_t *hrow = p.C + (size_t)m * half_n + n0 + 32 * wn + 4 * lg;
+                        uint8_t *hrow = p.C + (size_t)m * half_n + n0 + 64 * wn + 4 * lg;
 #pragma unroll
-                        for (int j = 0; j < 2; ++j)
+                        for (int j = 0; j < 4; ++j)
                             *reinterpret_cast<uint32_t *>(hrow + 16 * j) = f32x4_to_e4m3(
                                 h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv, h[i][j][3] * inv);
                         if (wn == 0 && lg == 0)
@@ -360,8 +395,10 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
     }
 }
 
-size_t gmm_lds_bytes() { return 4 * LDS_TILE + sizeof(GroupTable) + 2 * GTHREADS * sizeof(int); }
-// scratch holds 2*GTHREADS = 1024 ints: the group-table scan and the [4][256] fp8 amax exchange
+size_t gmm_lds_bytes()
+{
+    return GSTAGES * STAGE_BYTES + sizeof(GroupTable) + 2 * GTHREADS * sizeof(int) + 2 * G_MAX_NK * sizeof(float);
+}
 
 static int g_num_cus = 0;
 
