@@ -189,6 +189,40 @@ CAMHIP_API camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const
 CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                             void *stream);
 
+/* ------------------------------------------------------------------ fused decode entry
+ * Replaces aclnnFusedDeepMoe (fused_deep_moe/op_api/aclnn_fused_deep_moe.h:19-50;
+ * binding pybind/fused_deep_moe.cpp:30-83): dispatch + GMM1 + SwiGLU + GMM2 +
+ * combine (+ optional shared expert) in one stream-ordered call with fixed-size
+ * outputs and no host synchronisation, so it can be captured in a HIP graph.
+ * x [batchSize, hidden] bf16; expertIds [batchSize, topK] int32 in
+ * [-1, moeExpertNum) (-1: placeholder, not routed); expertScales [batchSize, topK]
+ * fp32 combine weights; xActiveMask [batchSize] bool (1 byte, true prefix) or NULL.
+ * Weights in coupled mode with the reduction dimension contiguous:
+ * gmm1Weight [L, gmm1HiddenSize, hidden] (rows [0,I) gate, [I,2I) up),
+ * gmm2Weight [L, hidden, gmm1HiddenSize/2]; weightDtype CAMHIP_DTYPE_BF16, or
+ * CAMHIP_DTYPE_FP8 with block scales [L, n/128, k/128] (activations are then
+ * quantised to fp8 1x128 on the fly).  The reference's int8 per-channel mode and
+ * smooth-quant scales are not supported by this build (NULL required).
+ * Shared expert (optional, all four given together): shareGmm1Weight
+ * [shareGmm1HiddenSize, hidden], shareGmm2Weight [hidden, shareGmm1HiddenSize/2]
+ * (+ scales [n/128, k/128] for fp8) -> shareOutput [batchSize, hidden] bf16.
+ * Outputs: output [batchSize, hidden] bf16; expertTokenNums [L] int64 (rows per
+ * local expert).  L = moeExpertNum / epRankSize; epRankSize must be 1 here.
+ * quantMode is reserved (0), as in the reference.  Limits
+ * (fused_deep_moe_tiling.cpp:59-75, widened where the GPU allows): batchSize
+ * <= 4096, topK <= 12, hidden in [1024,7168] and % 256 == 0, gmm1HiddenSize % 256 == 0. */
+CAMHIP_API camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
+    const uint16_t *x, const int32_t *expertIds, const void *gmm1Weight, const float *gmm1WeightScale,
+    const void *gmm2Weight, const float *gmm2WeightScale, const float *expertScales, const void *shareGmm1Weight,
+    const float *shareGmm1WeightScale, const void *shareGmm2Weight, const float *shareGmm2WeightScale,
+    const float *expertSmoothScales, const float *shareSmoothScales, const uint8_t *xActiveMask, int64_t batchSize,
+    int64_t hidden, int64_t topK, int64_t gmm1HiddenSize, int64_t shareGmm1HiddenSize, int64_t weightDtype,
+    int64_t epRankSize, int64_t epRankId, int64_t moeExpertNum, int64_t quantMode, int64_t globalBs,
+    uint16_t *output, uint16_t *shareOutput, int64_t *expertTokenNums, uint64_t *workspaceSize,
+    camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipFusedDeepMoe(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,7 @@ SIGNATURES = {
     "camhipMoeCombineNormal": "pp i pp iiiiii p",
     "camhipGroupedMatmulSwiglu": "ppp iiii pp ii pp",
     "camhipGroupedMatmul": "ppp iiii pp i p",
+    "camhipFusedDeepMoe": "pppppp p pppp ppp iiiiii iiiii ppp",
 }
 
 _lib = None

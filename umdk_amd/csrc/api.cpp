@@ -81,6 +81,34 @@ camhipStatus run_executor(const char *op, void *workspace, uint64_t workspaceSiz
     return st;
 }
 
+}  // namespace
+
+namespace cam {
+// shared with fused_api.cpp
+camhipStatus api_fail(camhipStatus code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+camhipStatus api_make_executor(uint64_t ws_bytes, std::function<hipError_t(void *, hipStream_t)> fn,
+                               uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    return make_executor(ws_bytes, std::move(fn), workspaceSize, executor);
+}
+camhipStatus api_run_executor(const char *op, void *workspace, uint64_t workspaceSize, camhipExecutor *ex,
+                              void *stream)
+{
+    return run_executor(op, workspace, workspaceSize, ex, stream);
+}
+}  // namespace cam
+
+namespace {
+
 constexpr int64_t kMaxTokens = 65536;
 constexpr int64_t kMaxExperts = 512;
 constexpr int64_t kMaxRanks = 384;

@@ -31,6 +31,8 @@ __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_id
                                              int cap, int lane)
 {
     int dst = -1;
+    if (topk_idx == nullptr)  // identity mode (K = 1): row t of x quantised into row t
+        return lane == 0 ? t : -1;
     if (lane < K) {
         const int e = topk_idx[(size_t)t * K + lane];
         if (e >= 0 && e < E) {
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
                 if (act1)
                     *reinterpret_cast<u32x4 *>(out + 512) = raw1;
             }
-            if (j == 0 && lane == 0) {
+            if (j == 0 && lane == 0 && expand_idx) {
                 expand_idx[(size_t)row * 3 + 0] = rank;
                 expand_idx[(size_t)row * 3 + 1] = t;
                 expand_idx[(size_t)row * 3 + 2] = k;
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
                 if ((lane & 7) == 0)
                     scales[(size_t)row * nb + (col >> 7)] = bscale;
             }
-            if (j == 0 && lane == 0) {
+            if (j == 0 && lane == 0 && expand_idx) {
                 expand_idx[(size_t)row * 3 + 0] = rank;
                 expand_idx[(size_t)row * 3 + 1] = t;
                 expand_idx[(size_t)row * 3 + 2] = k;
@@ -195,9 +197,11 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
         }
         if (lane == 0) {
             scales[row] = tok_scale;
-            expand_idx[(size_t)row * 3 + 0] = rank;
-            expand_idx[(size_t)row * 3 + 1] = t;
-            expand_idx[(size_t)row * 3 + 2] = k;
+            if (expand_idx) {
+                expand_idx[(size_t)row * 3 + 0] = rank;
+                expand_idx[(size_t)row * 3 + 1] = t;
+                expand_idx[(size_t)row * 3 + 2] = k;
+            }
         }
     }
 }

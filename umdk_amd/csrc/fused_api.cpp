@@ -1,0 +1,221 @@
+// camhipFusedDeepMoe: the decode entry of CAM (aclnnFusedDeepMoe,
+// fused_deep_moe/op_api/aclnn_fused_deep_moe.h:19-50; kernel
+// fused_deep_moe.h:355-448) on one GPU, composed from the path's kernels:
+//   prepare ids (x_active_mask, local expert range) -> layout -> count
+//   exchange -> quantised dispatch -> GMM1+SwiGLU -> GMM2 -> combine,
+//   plus the optional shared expert on all tokens.
+// Every intermediate lives in the caller's workspace and every size is fixed
+// by (batch, topk): no host synchronisation and no allocation, so the call can
+// be captured in a HIP graph (the reference's fused op is its graph-capturable
+// decode path, doc/en/cam/CAM API Guide.md:212).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <functional>
+#include <new>
+#include <string>
+
+#include "../../include/camhip.h"
+#include "gmm.h"
+#include "launchers.h"
+
+namespace cam {
+camhipStatus api_fail(camhipStatus code, const char *fmt, ...);
+camhipStatus api_make_executor(uint64_t ws_bytes, std::function<hipError_t(void *, hipStream_t)> fn,
+                               uint64_t *workspaceSize, camhipExecutor **executor);
+camhipStatus api_run_executor(const char *op, void *workspace, uint64_t workspaceSize, camhipExecutor *ex,
+                              void *stream);
+}  // namespace cam
+
+namespace {
+
+struct Carve {
+    uint64_t off = 0;
+    uint64_t take(uint64_t bytes)
+    {
+        const uint64_t o = off;
+        off += (bytes + 255) & ~(uint64_t)255;
+        return o;
+    }
+};
+
+struct FusedLayout {
+    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv;
+    uint64_t sh_x, sh_xs, sh_h, sh_hs, sh_gl;
+    uint64_t bytes;
+};
+
+FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, bool fp8, bool shared)
+{
+    Carve c;
+    FusedLayout f{};
+    const uint64_t N = (uint64_t)T * K;
+    const uint64_t esz = fp8 ? 1 : 2;
+    f.ids = c.take(4 * N);
+    f.layout_ws = c.take(cam::layout_workspace_bytes(T, K, L, 1));
+    f.counts = c.take(4 * (uint64_t)L);
+    f.send_off = c.take(4 * (uint64_t)L);
+    f.recv_cnt = c.take(4 * (uint64_t)L);
+    f.total = c.take(4);
+    f.sti = c.take(4 * N);
+    f.ex = c.take(N * H * esz);
+    f.xs = c.take(fp8 ? N * (H / 128) * 4 : 0);
+    f.eidx = c.take(12 * N);
+    f.h = c.take(N * I * esz);
+    f.hs = c.take(fp8 ? N * (I / 128) * 4 : 0);
+    f.y = c.take(N * H * 2);
+    f.inv = c.take(4 * N);
+    if (shared) {
+        f.sh_x = c.take((uint64_t)T * H * esz);
+        f.sh_xs = c.take(fp8 ? (uint64_t)T * (H / 128) * 4 : 0);
+        f.sh_h = c.take((uint64_t)T * Ish * esz);
+        f.sh_hs = c.take(fp8 ? (uint64_t)T * (Ish / 128) * 4 : 0);
+        f.sh_gl = c.take(8);
+    }
+    f.bytes = c.off;
+    return f;
+}
+
+#define F_CHECK(cond, ...)                                                                                          \
+    do {                                                                                                            \
+        if (!(cond))                                                                                                \
+            return cam::api_fail(CAMHIP_ERROR_INVALID_PARAM, __VA_ARGS__);                                          \
+    } while (0)
+#define F_PTR(p)                                                                                                    \
+    do {                                                                                                            \
+        if ((p) == nullptr)                                                                                         \
+            return cam::api_fail(CAMHIP_ERROR_NULLPTR, "fused_deep_moe: %s must not be NULL", #p);                  \
+    } while (0)
+
+#define HIP_TRY(x)                                                                                                  \
+    do {                                                                                                            \
+        hipError_t e_ = (x);                                                                                        \
+        if (e_ != hipSuccess)                                                                                       \
+            return e_;                                                                                              \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
+    const uint16_t *x, const int32_t *expertIds, const void *gmm1Weight, const float *gmm1WeightScale,
+    const void *gmm2Weight, const float *gmm2WeightScale, const float *expertScales, const void *shareGmm1Weight,
+    const float *shareGmm1WeightScale, const void *shareGmm2Weight, const float *shareGmm2WeightScale,
+    const float *expertSmoothScales, const float *shareSmoothScales, const uint8_t *xActiveMask, int64_t batchSize,
+    int64_t hidden, int64_t topK, int64_t gmm1HiddenSize, int64_t shareGmm1HiddenSize, int64_t weightDtype,
+    int64_t epRankSize, int64_t epRankId, int64_t moeExpertNum, int64_t quantMode, int64_t globalBs,
+    uint16_t *output, uint16_t *shareOutput, int64_t *expertTokenNums, uint64_t *workspaceSize,
+    camhipExecutor **executor)
+{
+    F_CHECK(epRankSize == 1 && epRankId == 0,
+            "fused_deep_moe: this build runs one EP rank per GPU (ep_rank_size %lld, ep_rank_id %lld; need 1, 0)",
+            (long long)epRankSize, (long long)epRankId);
+    F_CHECK(batchSize >= 0 && batchSize <= 4096, "fused_deep_moe: batch size %lld out of [0,4096]",
+            (long long)batchSize);
+    F_CHECK(topK >= 1 && topK <= 12, "fused_deep_moe: topk %lld out of [1,12]", (long long)topK);
+    F_CHECK(moeExpertNum >= 1 && moeExpertNum <= 512 && topK <= moeExpertNum,
+            "fused_deep_moe: moe_expert_num %lld out of [topk,512]", (long long)moeExpertNum);
+    F_CHECK(hidden >= 1024 && hidden <= 7168 && hidden % 256 == 0,
+            "fused_deep_moe: hidden %lld must be in [1024,7168] and a multiple of 256", (long long)hidden);
+    F_CHECK(gmm1HiddenSize >= 256 && gmm1HiddenSize % 256 == 0,
+            "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
+    F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_FP8,
+            "fused_deep_moe: weight dtype %lld not supported (bf16 or fp8 e4m3fn)", (long long)weightDtype);
+    F_CHECK(quantMode == 0, "fused_deep_moe: quant_mode is reserved and must be 0 (got %lld)", (long long)quantMode);
+    F_CHECK(globalBs >= 0 && globalBs % epRankSize == 0, "fused_deep_moe: global_bs %lld invalid",
+            (long long)globalBs);
+    F_CHECK(expertSmoothScales == nullptr && shareSmoothScales == nullptr,
+            "fused_deep_moe: smooth-quant scales are not supported by this build");
+    const bool shared = shareGmm1Weight != nullptr;
+    F_CHECK(shared == (shareGmm2Weight != nullptr),
+            "fused_deep_moe: shared-expert weights must be given together");
+    const bool fp8 = weightDtype == CAMHIP_DTYPE_FP8;
+    if (shared) {
+        F_CHECK(shareGmm1HiddenSize >= 256 && shareGmm1HiddenSize % 256 == 0,
+                "fused_deep_moe: share gmm1 hidden size %lld must be a multiple of 256",
+                (long long)shareGmm1HiddenSize);
+        F_PTR(shareOutput);
+        if (fp8) {
+            F_PTR(shareGmm1WeightScale);
+            F_PTR(shareGmm2WeightScale);
+        }
+    }
+    F_PTR(gmm1Weight);
+    F_PTR(gmm2Weight);
+    F_PTR(expertTokenNums);
+    if (fp8) {
+        F_PTR(gmm1WeightScale);
+        F_PTR(gmm2WeightScale);
+    }
+    if (batchSize > 0) {
+        F_PTR(x);
+        F_PTR(expertIds);
+        F_PTR(expertScales);
+        F_PTR(output);
+    }
+    F_CHECK(workspaceSize != nullptr && executor != nullptr, "fused_deep_moe: NULL workspace size or executor");
+
+    const int T = (int)batchSize, H = (int)hidden, K = (int)topK, L = (int)(moeExpertNum / epRankSize);
+    const int I = (int)(gmm1HiddenSize / 2), Ish = (int)(shareGmm1HiddenSize / 2);
+    const FusedLayout f = plan_fused(T, H, K, L, I, shared ? Ish : 0, fp8, shared);
+    const int N = T * K;
+    const int dt = fp8 ? cam::DT_FP8 : cam::DT_BF16;
+    const int q = fp8 ? cam::QUANT_FP8_BLOCK : cam::QUANT_NONE;
+    const int epi1 = fp8 ? cam::EPI_SWIGLU_FP8 : cam::EPI_SWIGLU_BF16;
+
+    auto fn = [=](void *wsv, hipStream_t s) -> hipError_t {
+        uint8_t *ws = (uint8_t *)wsv;
+        auto P = [&](uint64_t off) { return (void *)(ws + off); };
+        int32_t *ids = (int32_t *)P(f.ids);
+        int32_t *counts = (int32_t *)P(f.counts), *send_off = (int32_t *)P(f.send_off);
+        int32_t *recv_cnt = (int32_t *)P(f.recv_cnt);
+        if (T == 0) {  // no tokens: no expert receives any
+            return cam::launch_fill_i64(expertTokenNums, 0, L, s);
+        }
+        HIP_TRY(cam::launch_prepare_ids(expertIds, xActiveMask, T, K, 0, L, ids, s));
+        HIP_TRY(cam::launch_layout_i32(ids, T, K, L, counts, (int32_t *)P(f.sti), P(f.layout_ws), s));
+        HIP_TRY(cam::launch_notify(counts, L, T, send_off, (int32_t *)P(f.total), recv_cnt, nullptr, nullptr,
+                                   expertTokenNums, L, s));
+        HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
+                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s));
+        cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
+                        (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
+        HIP_TRY(cam::launch_gmm(g1, dt, epi1, s));
+        cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
+                        (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
+        HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
+        HIP_TRY(cam::launch_combine((const uint16_t *)P(f.y), (const int32_t *)P(f.eidx), N, recv_cnt + (L - 1),
+                                    expertScales, T, K, H, output, (int32_t *)P(f.inv), s));
+        if (shared) {
+            // shared expert on every token: x quantised in token order, one group of T rows
+            int64_t *gl = (int64_t *)P(f.sh_gl);
+            HIP_TRY(cam::launch_fill_i64(gl, T, 1, s));
+            const void *sx = x;
+            const float *sxs = nullptr;
+            if (fp8) {
+                HIP_TRY(cam::launch_dispatch(x, nullptr, nullptr, nullptr, T, H, 1, 1, 0, T, q, P(f.sh_x),
+                                             (float *)P(f.sh_xs), nullptr, s));
+                sx = P(f.sh_x);
+                sxs = (const float *)P(f.sh_xs);
+            }
+            cam::GmmArgs s1{(const uint8_t *)sx, sxs, gl, 1, T, H, 2 * Ish, (const uint8_t *)shareGmm1Weight,
+                            shareGmm1WeightScale, (uint8_t *)P(f.sh_h), (float *)P(f.sh_hs)};
+            HIP_TRY(cam::launch_gmm(s1, dt, epi1, s));
+            cam::GmmArgs s2{(const uint8_t *)P(f.sh_h), (const float *)P(f.sh_hs), gl, 1, T, Ish, H,
+                            (const uint8_t *)shareGmm2Weight, shareGmm2WeightScale, (uint8_t *)shareOutput,
+                            nullptr};
+            HIP_TRY(cam::launch_gmm(s2, dt, cam::EPI_PLAIN, s));
+        }
+        return hipSuccess;
+    };
+    return cam::api_make_executor(f.bytes, fn, workspaceSize, executor);
+}
+
+camhipStatus camhipFusedDeepMoe(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return cam::api_run_executor("fused_deep_moe", workspace, workspaceSize, executor, stream);
+}
+
+}  // extern "C"

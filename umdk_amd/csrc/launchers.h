@@ -34,10 +34,15 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
                          int32_t *recv_count, int32_t *recv_offset, int32_t *max_bs,
                          int64_t *recv_tokens_per_expert, int local_experts, hipStream_t s);
 
-// ---- permute + quantise (dispatch.hip)
+// ---- permute + quantise (dispatch.hip); topk_idx == nullptr: identity rows (K must be 1)
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s);
+
+// ---- fused decode helpers (fused.hip)
+hipError_t launch_prepare_ids(const int32_t *ids, const uint8_t *active, int T, int K, int first_local, int L,
+                              int32_t *out, hipStream_t s);
+hipError_t launch_fill_i64(int64_t *p, int64_t v, long n, hipStream_t s);
 
 // ---- weighted unpermute (combine.hip)
 hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,

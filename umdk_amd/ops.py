@@ -39,7 +39,17 @@ _def.define("grouped_matmul_swiglu(Tensor x, Tensor? x_scale, Tensor group_list,
 _def.define("grouped_matmul(Tensor x, Tensor? x_scale, Tensor group_list, Tensor weight, Tensor? weight_scale) "
             "-> Tensor")
 
+_def.define(
+    "fused_deep_moe(Tensor x, Tensor expert_ids, Tensor[] gmm1_weight, Tensor[] gmm1_weight_scale, "
+    "Tensor[] gmm2_weight, Tensor[] gmm2_weight_scale, Tensor expert_scales, "
+    "Tensor? share_gmm1_weight, Tensor? share_gmm1_weight_scale, "
+    "Tensor? share_gmm2_weight, Tensor? share_gmm2_weight_scale, "
+    "Tensor? expert_smooth_scales, Tensor? share_smooth_scales, Tensor? x_active_mask, "
+    "str group_ep, int ep_rank_size, int ep_rank_id, int moe_expert_num, "
+    "int quant_mode, int global_bs) -> Tensor[]")
+
 _impl = torch.library.Library(LIB_NAME, "IMPL", "CUDA")
+_meta = torch.library.Library(LIB_NAME, "IMPL", "Meta")
 
 QUANT_NONE, QUANT_INT8_TOKEN, QUANT_FP8_BLOCK = 0, 2, 3
 
@@ -244,6 +254,111 @@ def prepack_weight(w_lkn):
     return w_lkn.transpose(1, 2).contiguous()
 
 
+def _kmajor(w, n, k, what):
+    """A weight given in the reference's logical [..., k, n] shape -> storage with k contiguous
+    ([..., n, k]).  A transposed view of such storage is used as is; a contiguous [..., k, n]
+    tensor is transposed once (a copy)."""
+    if tuple(w.shape[-2:]) == (k, n) and w.stride(-2) == 1 and w.stride(-1) == k:
+        return w.transpose(-1, -2)          # already k-contiguous underneath: no copy
+    if tuple(w.shape[-2:]) == (k, n):
+        return w.transpose(-1, -2).contiguous()
+    raise RuntimeError(f"fused_deep_moe: {what} must have logical shape [..., {k}, {n}], got {tuple(w.shape)}")
+
+
+def _coupled(ws, L, n, k, what):
+    if len(ws) == 1 and ws[0].dim() == 3:
+        w = _kmajor(ws[0], n, k, what)
+    else:
+        _check(len(ws) == L, f"fused_deep_moe: {what} needs 1 coupled tensor or {L} per-expert tensors")
+        w = torch.stack([_kmajor(t, n, k, what) for t in ws])   # separated mode: one copy per call
+    _check(tuple(w.shape) == (L, n, k), f"fused_deep_moe: {what} shape mismatch")
+    return w.contiguous()
+
+
+def _scales(ss, L, n, k, what):
+    if not ss or ss[0] is None:
+        return None
+    s = ss[0] if (len(ss) == 1 and ss[0].dim() == 3) else torch.stack(list(ss))
+    _check(s.dtype == torch.float32 and tuple(s.shape) == (L, n // 128, k // 128),
+           f"fused_deep_moe: {what} must be float32 [{L}, {n // 128}, {k // 128}] (128x128 block scales)")
+    return s.contiguous()
+
+
+def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, gmm2_weight_scale, expert_scales,
+                   share_gmm1_weight, share_gmm1_weight_scale, share_gmm2_weight, share_gmm2_weight_scale,
+                   expert_smooth_scales, share_smooth_scales, x_active_mask, group_ep, ep_rank_size, ep_rank_id,
+                   moe_expert_num, quant_mode, global_bs):
+    """Decode MoE layer in one call: dispatch + GMM1 + SwiGLU + GMM2 + combine
+    (+ shared expert), returning [output, share_output, expert_token_nums].
+
+    Mirrors FusedDeepMoeImplNpu (pybind/fused_deep_moe.cpp:30-83) and the API
+    guide (doc/en/cam/CAM API Guide.md:177-226): weights in the logical
+    [L, H, 2I] / [L, I, H] shapes (one coupled tensor or L separated ones;
+    a transposed view of k-contiguous storage avoids a copy), expert_ids
+    int32 with -1 placeholders, x_active_mask a true-prefix bool mask.
+    Weights are bf16, or float8_e4m3fn with 128x128 block scales
+    [L, n/128, k/128]; the reference's int8 per-channel weights and the
+    smooth-quant scales are not supported here.  Output shapes are fixed by
+    the inputs, so the op can be captured in a graph."""
+    _check(x.dim() == 2 and x.dtype == torch.bfloat16 and x.is_contiguous(),
+           "fused_deep_moe: x must be a contiguous [batch, hidden] bfloat16 tensor")
+    _check(expert_ids.dim() == 2, "fused_deep_moe: expert_ids must be 2-D")
+    _single_rank(ep_rank_id, ep_rank_size, "fused_deep_moe")
+    bs, h = x.shape
+    k = expert_ids.shape[1]
+    L = moe_expert_num // ep_rank_size
+    dt = gmm1_weight[0].dtype
+    _check(dt in (torch.bfloat16, torch.float8_e4m3fn),
+           f"fused_deep_moe: weight dtype {dt} not supported (bfloat16 or float8_e4m3fn; int8 per-channel "
+           "weights of the reference are not supported by this build)")
+    w1_logical = gmm1_weight[0].shape
+    n1 = w1_logical[-1]
+    I = n1 // 2
+    w1 = _coupled(gmm1_weight, L, n1, h, "gmm1_weight")
+    w2 = _coupled(gmm2_weight, L, h, I, "gmm2_weight")
+    fp8 = dt == torch.float8_e4m3fn
+    s1 = _scales(gmm1_weight_scale, L, n1, h, "gmm1_weight_scale") if fp8 else None
+    s2 = _scales(gmm2_weight_scale, L, h, I, "gmm2_weight_scale") if fp8 else None
+    shared = share_gmm1_weight is not None
+    sw1 = sw2 = ss1 = ss2 = None
+    nsh = 0
+    if shared:
+        _check(share_gmm2_weight is not None, "fused_deep_moe: share_gmm2_weight missing")
+        nsh = share_gmm1_weight.shape[-1]
+        sw1 = _kmajor(share_gmm1_weight, nsh, h, "share_gmm1_weight").contiguous()
+        sw2 = _kmajor(share_gmm2_weight, h, nsh // 2, "share_gmm2_weight").contiguous()
+        if fp8:
+            ss1 = share_gmm1_weight_scale.contiguous()
+            ss2 = share_gmm2_weight_scale.contiguous()
+    ids = expert_ids if expert_ids.dtype == torch.int32 else expert_ids.to(torch.int32)
+    ids = ids.contiguous()
+    es = expert_scales if expert_scales.dtype == torch.float32 else expert_scales.to(torch.float32)
+    es = es.contiguous()
+    mask = None
+    if x_active_mask is not None:
+        mask = x_active_mask.to(torch.bool).contiguous().view(torch.uint8)
+    out = torch.empty_like(x)
+    share_out = torch.empty_like(x)
+    etn = torch.empty(L, dtype=torch.int64, device=x.device)
+    _lib.call("camhipFusedDeepMoe", _lib.ptr(x), _lib.ptr(ids), _lib.ptr(w1), _lib.ptr(s1), _lib.ptr(w2),
+              _lib.ptr(s2), _lib.ptr(es), _lib.ptr(sw1), _lib.ptr(ss1), _lib.ptr(sw2), _lib.ptr(ss2),
+              _lib.ptr(expert_smooth_scales), _lib.ptr(share_smooth_scales), _lib.ptr(mask), bs, h, k, n1, nsh,
+              3 if fp8 else 0, ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs, _lib.ptr(out),
+              _lib.ptr(share_out), _lib.ptr(etn), device=x.device)
+    return [out, share_out, etn]
+
+
+def fused_deep_moe_meta(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, gmm2_weight_scale,
+                        expert_scales, share_gmm1_weight, share_gmm1_weight_scale, share_gmm2_weight,
+                        share_gmm2_weight_scale, expert_smooth_scales, share_smooth_scales, x_active_mask, group_ep,
+                        ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs):
+    """Shape function (pybind/fused_deep_moe.cpp:91-124)."""
+    L = moe_expert_num // ep_rank_size
+    return [torch.empty_like(x), torch.empty_like(x), torch.empty(L, dtype=torch.int64, device=x.device)]
+
+
+_impl.impl("fused_deep_moe", fused_deep_moe)
+_meta.impl("fused_deep_moe", fused_deep_moe_meta)
 _impl.impl("grouped_matmul_swiglu", grouped_matmul_swiglu)
 _impl.impl("grouped_matmul", grouped_matmul)
 _impl.impl("get_dispatch_layout", get_dispatch_layout)
