@@ -190,6 +190,67 @@ def gemm_sweep(steps, warmup, seed):
     return out
 
 
+def run_decode(steps, seed):
+    """Config 5: decode step (T=128, H=7168, route over 256 experts, 32 local experts, I=2048, fp8)
+    = route + fused_deep_moe captured in one HIP graph; p50/p99 of single-replay times."""
+    import numpy as np
+
+    from umdk_amd import _lib
+    T, H, E, K, L, I = 128, 7168, 256, 8, 32, 2048
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).bfloat16().to(dev)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    w1, s1, w2, s2 = make_weights(L, H, I, "fp8", dev, seed)
+    ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+    wts = torch.empty(T, K, dtype=torch.float32, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    share = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    etn = torch.empty(L, dtype=torch.int64, device=dev)
+    fargs = (x.data_ptr(), ids.data_ptr(), w1.data_ptr(), s1.data_ptr(), w2.data_ptr(), s2.data_ptr(),
+             wts.data_ptr(), None, None, None, None, None, None, None, T, H, K, 2 * I, 0, 3, 1, 0, L, 0, 0,
+             out.data_ptr(), share.data_ptr(), etn.data_ptr())
+    ws = torch.empty(_lib.workspace_size("camhipFusedDeepMoe", *fargs), dtype=torch.uint8, device=dev)
+
+    def step():
+        # routing over all 256 experts; ids of the 224 non-local experts are not routed on this rank
+        _lib.launch("camhipMoeRoute", logits.data_ptr(), None, T, E, K, ids.data_ptr(), wts.data_ptr(),
+                    device=dev)
+        _lib.launch("camhipFusedDeepMoe", *fargs, workspace=ws, device=dev)
+
+    st = torch.cuda.Stream(device=dev)
+    st.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream(dev).wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(20):
+        graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    times = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    counts = etn.cpu()
+    touched = int((counts > 0).sum())
+    wbytes = touched * 3 * H * I   # fp8 W1 (2I x H) + W2 (H x I) of touched experts
+    p50 = float(np.percentile(times, 50))
+    return {"workload": "config5: decode step, route + fused_deep_moe in one HIP graph, fp8", "tokens": T,
+            "hidden": H, "experts_routed": E, "local_experts": L, "topk": K, "intermediate": I,
+            "replays": steps, "p50_us": p50, "p99_us": float(np.percentile(times, 99)),
+            "mean_us": float(times.mean()), "local_rows": int(counts.sum()), "experts_touched": touched,
+            "weight_bytes_touched": wbytes, "weight_GBps_at_p50": wbytes / (p50 * 1e-6) / 1e9,
+            "hbm_roofline_frac": (wbytes / (HBM_PEAK_GBPS * 1e9)) / (p50 * 1e-6)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,7 +258,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="2", choices=["2", "3", "4", "sweep", "all"],
+    ap.add_argument("--config", default="2", choices=["2", "3", "4", "5", "sweep", "all"],
                     help="2: dispatch+combine headline (default; also reports configs 3 and 4 briefly); "
                          "3/4: only that layer config; sweep: fp8 grouped-GEMM M-sweep")
     ap.add_argument("--calib-copy", action="store_true",
@@ -223,8 +284,9 @@ def main():
                                     "bf16", st, wu, args.seed, None)
     cfg4 = lambda st, wu: run_layer("config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), fp8",
                                     4096, 7168, 256, 8, 32, 2048, "fp8", st, wu, args.seed, "zipf")
-    if args.config in ("3", "4", "sweep"):
+    if args.config in ("3", "4", "5", "sweep"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
+             "5": lambda: run_decode(max(args.steps, 1000), args.seed),
              "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed)}[args.config]()
         print(json.dumps({"config": args.config, "result": r}))
         return
@@ -304,6 +366,8 @@ def main():
         result["config3"] = cfg3(10, 3)
         torch.cuda.empty_cache()
         result["config4"] = cfg4(20, 5)
+        torch.cuda.empty_cache()
+        result["config5"] = run_decode(1000, args.seed)
         torch.cuda.empty_cache()
     if args.config == "all":
         result["fp8_gemm_sweep"] = gemm_sweep(10, 3, args.seed)
