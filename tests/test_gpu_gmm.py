@@ -56,7 +56,8 @@ def dq_rows(q, s):
     return (q.float().view(m, k // 128, 128) * s.float().view(m, k // 128, 1)).view(m, k)
 
 
-SMALL = [([5, 0, 300], 256, 256), ([1], 128 * 4, 128), ([17, 256, 255, 1, 0, 9], 512, 128)]
+# the first two cases take the 32-row tile (rows <= 48 per expert), the others the 128-row tile
+SMALL = [([3, 40, 0, 7], 1024, 256), ([1], 128 * 4, 128), ([5, 0, 300], 256, 256), ([17, 256, 255, 1, 0, 9], 512, 128)]
 
 
 @pytest.mark.parametrize("counts,H,I", SMALL)

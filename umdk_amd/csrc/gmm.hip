@@ -46,18 +46,29 @@ namespace cam {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
-constexpr int GBM = 128, GBN = 256, GKB = 128;  // tile rows, tile W-rows, bytes per row per k-step
-constexpr int GTHREADS = 256;
-constexpr int GSTAGES = 3;
+constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
+constexpr int GTHREADS = 256;        // 4 waves
 constexpr int G_MAX_L = 512;
-constexpr int A_BYTES = GBM * GKB;           // 16 KiB
-constexpr int B_BYTES = GBN * GKB;           // 32 KiB
-constexpr int S_BYTES = 4 * 64 * 4;          // per-wave copies of 64 activation scales
-constexpr int STAGE_BYTES = A_BYTES + B_BYTES + S_BYTES;
-constexpr int A_LOADS = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage (1 KiB each)
-constexpr int B_LOADS = B_BYTES / 1024 / 4;
+constexpr int G_MAX_NK = 256;        // fp8 k <= 32768
 
-constexpr int G_MAX_NK = 256;                // fp8 k <= 32768
+// Tile shapes.  BM = 128: 2 x 2 waves of 64 x 128, 3-stage ring (prefill: many rows per expert).
+// BM = 32: 1 x 4 waves of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the
+// k-loop is a weight stream and the extra stage keeps more of it in flight).
+template <int BM_> struct Tile {
+    static constexpr int BM = BM_;
+    static constexpr int WAVES_M = BM >= 128 ? 2 : 1;
+    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int WM = BM / WAVES_M, WN = GBN / WAVES_N;  // wave tile
+    static constexpr int IF = WM / 16, JF = WN / 16;              // MFMA fragments per wave
+    static constexpr int STAGES = BM >= 128 ? 3 : 4;
+    static constexpr int A_BYTES = BM * GKB;
+    static constexpr int B_BYTES = GBN * GKB;
+    static constexpr int S_BYTES = 4 * 64 * 4;   // per-wave copies of 64 activation scales
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int A_LOADS = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage (1 KiB each)
+    static constexpr int B_LOADS = B_BYTES / 1024 / 4;
+    static_assert(WM <= 64, "one 64-lane scale DMA per wave covers its rows");
+};
 
 struct GroupTable {
     int tile_prefix[G_MAX_L + 1];  // exclusive prefix of M-tiles per expert
@@ -65,6 +76,7 @@ struct GroupTable {
 };
 
 // Block-wide exclusive scans of ceil(cnt/GBM) and cnt over the L experts.
+template <int GBM>
 __device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch)
 {
     const int tid = threadIdx.x;
@@ -133,19 +145,23 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
 }
 
-template <int DT, int EPI>
+template <int DT, int EPI, int BM>
 __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
 {
+    using TC = Tile<BM>;
+    constexpr int GBM = TC::BM, WM = TC::WM, WN = TC::WN, IF = TC::IF, JF = TC::JF;
+    constexpr int GSTAGES = TC::STAGES, STAGE_BYTES = TC::STAGE_BYTES;
+    constexpr int A_BYTES = TC::A_BYTES, B_BYTES = TC::B_BYTES, A_LOADS = TC::A_LOADS, B_LOADS = TC::B_LOADS;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
     int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GTHREADS ints: table scan, then the fp8 amax exchange
     float *wsc = reinterpret_cast<float *>(scratch + 2 * GTHREADS);  // [2][G_MAX_NK] weight scales of the tile
 
-    build_group_table(p.group_list, p.L, *gt, scratch);
+    build_group_table<GBM>(p.group_list, p.L, *gt, scratch);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = w >> 1, wn = w & 1;
+    const int wm = w / TC::WAVES_N, wn = w % TC::WAVES_N;
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
     constexpr bool FP8 = DT == DT_FP8;
@@ -192,7 +208,7 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
         uint32_t ga[A_LOADS], gb[B_LOADS];
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int r = (i * 4 + w) * 8 + band_row;  // tile row 0..127
+            const int r = (i * 4 + w) * 8 + band_row;  // tile row 0..GBM-1
             ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off;
         }
 #pragma unroll
@@ -200,18 +216,18 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
             const int r = (i * 4 + w) * 8 + band_row;  // LDS W row 0..255
             int wrow;
             if (SWIGLU) {
-                // LDS rows [128 c, 128 c + 128) feed column wave c: 64 gate rows, then the
-                // 64 up rows of the same h-columns
-                const int c = r >> 7, jj = r & 127;
-                const int hcol = n0 + 64 * c + (jj & 63);
-                wrow = jj < 64 ? hcol : half_n + hcol;
+                // LDS rows [WN c, WN c + WN) feed column wave c: WN/2 gate rows, then the
+                // WN/2 up rows of the same h-columns
+                const int c = r / WN, jj = r % WN;
+                const int hcol = n0 + (WN / 2) * c + (jj % (WN / 2));
+                wrow = jj < WN / 2 ? hcol : half_n + hcol;
             } else {
                 wrow = n0 + r;
             }
             gb[i] = (uint32_t)wrow * kbytes + chunk_off;
         }
-        // fp8: this wave's 64 activation-scale rows (rows of its row half wm)
-        const uint32_t gs = (uint32_t)min(row0 + wm * 64 + lane, p.M - 1) * (uint32_t)nk;
+        // fp8: this wave's activation-scale rows (the WM rows of its row block wm; 64 lanes)
+        const uint32_t gs = (uint32_t)min(row0 + wm * WM + lane, p.M - 1) * (uint32_t)nk;
 
         auto issue = [&](int ks, int slot) {
             const int kc = min(ks, nk - 1);  // past the end: reload the last k-step (keeps the count uniform)
@@ -226,11 +242,11 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 dma4(p.As + gs + kc, st + A_BYTES + B_BYTES + w * 256);
         };
 
-        f32x4 acc[4][8];
+        f32x4 acc[IF][JF];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < IF; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < JF; ++j)
                 acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         if constexpr (FP8) {
@@ -245,31 +261,32 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
             }
             __syncthreads();
         }
-        const float *ws_g = wsc + (SWIGLU ? 0 : wn * G_MAX_NK);
+        const float *ws_g = wsc + (SWIGLU ? 0 : ((wn * WN) / 128) * G_MAX_NK);
         const float *ws_u = wsc + G_MAX_NK;
 
-        issue(0, 0);
-        issue(1, 1);
+#pragma unroll
+        for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
+            issue(s0, s0);
         for (int ks = 0; ks < nk; ++ks) {
             const int cur = ks % GSTAGES;
-            wait_vmcnt<LOADS>();  // this wave's DMA for k-step ks has landed
-            bar();                // ... and every other wave's; slot (ks+2)%3 is free again
-            issue(ks + 2, (ks + 2) % GSTAGES);
+            wait_vmcnt<LOADS *(GSTAGES - 2)>();  // this wave's DMA for k-step ks has landed
+            bar();  // ... and every other wave's; the slot of k-step ks-1 is free again
+            issue(ks + GSTAGES - 1, (ks + GSTAGES - 1) % GSTAGES);
             const uint8_t *st = smem + cur * STAGE_BYTES;
-            const uint8_t *la = st + (wm * 64) * GKB;
-            const uint8_t *lb = st + A_BYTES + (wn * 128) * GKB;
+            const uint8_t *la = st + (wm * WM) * GKB;
+            const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
             if constexpr (DT == DT_BF16) {
 #pragma unroll
                 for (int sub = 0; sub < 2; ++sub) {
-                    bf16x8 afr[4];
+                    bf16x8 afr[IF];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < IF; ++i)
                         afr[i] = *reinterpret_cast<const bf16x8 *>(la + swz(i * 16 + l16, sub * 4 + lg));
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
+                    for (int j = 0; j < JF; ++j) {
                         const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
+                        for (int i = 0; i < IF; ++i)
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, afr[i], acc[i][j], 0, 0, 0);
                     }
                 }
@@ -277,10 +294,10 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * 256);
                 const float sg = ws_g[ks];
                 const float su = SWIGLU ? ws_u[ks] : sg;
-                float sa[4];
-                i32x8 afr[4];
+                float sa[IF];
+                i32x8 afr[IF];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < IF; ++i) {
                     sa[i] = sst[i * 16 + l16];
                     const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
                     const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
@@ -288,15 +305,15 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                                    (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                 }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < JF; ++j) {
                     const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg));
                     const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg + 1));
                     const i32x8 bfr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                             (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                    // in SwiGLU tiles a wave's columns j<4 are gate rows, j>=4 up rows
-                    const float sw = (SWIGLU && j >= 4) ? su : sg;
+                    // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
+                    const float sw = (SWIGLU && j >= JF / 2) ? su : sg;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
+                    for (int i = 0; i < IF; ++i) {
                         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                         const f32x4 d =
                             __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr, afr[i], z, 0, 0, 0, 127, 0, 127);
@@ -311,17 +328,17 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
         wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
         bar();
 
-        // ---- epilogue: lane holds rows m = row0 + wm*64 + 16 i + l16 and, per j, four
-        // consecutive columns 16 j + 4 lg + q of the wave's 128-wide column range
+        // ---- epilogue: lane holds rows m = row0 + wm*WM + 16 i + l16 and, per j, four
+        // consecutive columns 16 j + 4 lg + q of the wave's WN-wide column range
         if constexpr (EPI == EPI_PLAIN) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = row0 + wm * 64 + i * 16 + l16;
+            for (int i = 0; i < IF; ++i) {
+                const int m = row0 + wm * WM + i * 16 + l16;
                 if (m >= seg1)
                     continue;
-                uint16_t *crow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * p.N + n0 + wn * 128 + 4 * lg;
+                uint16_t *crow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * p.N + n0 + wn * WN + 4 * lg;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < JF; ++j) {
                     u32x2 v;
                     v[0] = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
                     v[1] = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
@@ -329,26 +346,28 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 }
             }
         } else {
-            // h-columns of this wave: n0 + 64 wn + 16 j + 4 lg + q, j < 4 (gate j, up j+4)
-            float h[4][4][4];
+            // h-columns of this wave: n0 + (WN/2) wn + 16 j + 4 lg + q, j < JF/2 (gate j, up j+JF/2)
+            constexpr int HF = JF / 2;
+            float h[IF][HF][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < IF; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < HF; ++j)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const float g = acc[i][j][q], u = acc[i][j + 4][q];
+                        const float g = acc[i][j][q], u = acc[i][j + HF][q];
                         h[i][j][q] = g / (1.0f + expf(-g)) * u;
                     }
             if constexpr (EPI == EPI_SWIGLU_BF16) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = row0 + wm * 64 + i * 16 + l16;
+                for (int i = 0; i < IF; ++i) {
+                    const int m = row0 + wm * WM + i * 16 + l16;
                     if (m >= seg1)
                         continue;
-                    uint16_t *hrow = reinterpret_cast<uint16_t *>(p.C) + (size_t)m * half_n + n0 + 64 * wn + 4 * lg;
+                    uint16_t *hrow =
+                        reinterpret_cast<uint16_t *>(p.C) + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < HF; ++j) {
                         u32x2 v;
                         v[0] = f32_to_bf16(h[i][j][0]) | (f32_to_bf16(h[i][j][1]) << 16);
                         v[1] = f32_to_bf16(h[i][j][2]) | (f32_to_bf16(h[i][j][3]) << 16);
@@ -357,32 +376,35 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
                 }
             } else {
                 // fp8 1x128 requant: the tile's 128 h-columns of a row are one scale block,
-                // split over the two column waves; exchange partial amax through LDS
-                float *red = reinterpret_cast<float *>(scratch);  // [2][128]
+                // split over the column waves; exchange partial amax through LDS
+                float *red = reinterpret_cast<float *>(scratch);  // [WAVES_N][GBM]
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < IF; ++i) {
                     float mx = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < HF; ++j)
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
                             mx = fmaxf(mx, fabsf(h[i][j][q]));
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                     if (lg == 0)
-                        red[wn * 128 + wm * 64 + i * 16 + l16] = mx;
+                        red[wn * GBM + wm * WM + i * 16 + l16] = mx;
                 }
                 __syncthreads();
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = wm * 64 + i * 16 + l16;
+                for (int i = 0; i < IF; ++i) {
+                    const int r = wm * WM + i * 16 + l16;
                     const int m = row0 + r;
-                    const float amax = fmaxf(fmaxf(red[r], red[128 + r]), 1e-4f);
+                    float amax = 1e-4f;
+#pragma unroll
+                    for (int c = 0; c < TC::WAVES_N; ++c)
+                        amax = fmaxf(amax, red[c * GBM + r]);
                     const float inv = 448.0f / amax;
                     if (m < seg1) {
-                        uint8_t *hrow = p.C + (size_t)m * half_n + n0 + 64 * wn + 4 * lg;
+                        uint8_t *hrow = p.C + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
+                        for (int j = 0; j < HF; ++j)
                             *reinterpret_cast<uint32_t *>(hrow + 16 * j) = f32x4_to_e4m3(
                                 h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv, h[i][j][3] * inv);
                         if (wn == 0 && lg == 0)
@@ -395,19 +417,24 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
     }
 }
 
-size_t gmm_lds_bytes()
+template <int BM> static size_t lds_bytes()
 {
-    return GSTAGES * STAGE_BYTES + sizeof(GroupTable) + 2 * GTHREADS * sizeof(int) + 2 * G_MAX_NK * sizeof(float);
+    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GTHREADS * sizeof(int) +
+           2 * G_MAX_NK * sizeof(float);
 }
+static_assert(sizeof(GroupTable) + 2 * GTHREADS * 4 + 2 * G_MAX_NK * 4 + 3 * Tile<128>::STAGE_BYTES <= 163840, "LDS");
+static_assert(sizeof(GroupTable) + 2 * GTHREADS * 4 + 2 * G_MAX_NK * 4 + 4 * Tile<32>::STAGE_BYTES <= 163840, "LDS");
+
+size_t gmm_lds_bytes() { return lds_bytes<128>() > lds_bytes<32>() ? lds_bytes<128>() : lds_bytes<32>(); }
 
 static int g_num_cus = 0;
 
-template <int DT, int EPI> static hipError_t launch_one(const GmmArgs &a, hipStream_t s)
+template <int DT, int EPI, int BM> static hipError_t launch_bm(const GmmArgs &a, hipStream_t s)
 {
     static bool attr_set = false;
-    const size_t lds = gmm_lds_bytes();
+    const size_t lds = lds_bytes<BM>();
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)gmm_kernel<DT, EPI>,
+        hipError_t e = hipFuncSetAttribute((const void *)gmm_kernel<DT, EPI, BM>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess)
             return e;
@@ -422,8 +449,17 @@ template <int DT, int EPI> static hipError_t launch_one(const GmmArgs &a, hipStr
             g_num_cus = 256;
     }
     const int grid = (g_num_cus + 7) / 8 * 8;
-    hipLaunchKernelGGL((gmm_kernel<DT, EPI>), dim3(grid), dim3(GTHREADS), lds, s, a);
+    hipLaunchKernelGGL((gmm_kernel<DT, EPI, BM>), dim3(grid), dim3(GTHREADS), lds, s, a);
     return hipGetLastError();
+}
+
+// Tile choice from the row capacity per expert: segments of a few rows (decode) get the 32-row
+// tile, whose k-loop is nearly all weight bytes.
+template <int DT, int EPI> static hipError_t launch_one(const GmmArgs &a, hipStream_t s)
+{
+    if (a.M <= 48 * a.L)
+        return launch_bm<DT, EPI, 32>(a, s);
+    return launch_bm<DT, EPI, 128>(a, s);
 }
 
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
