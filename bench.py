@@ -258,9 +258,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="2", choices=["2", "3", "4", "5", "sweep", "all"],
-                    help="2: dispatch+combine headline (default; also reports configs 3 and 4 briefly); "
-                         "3/4: only that layer config; sweep: fp8 grouped-GEMM M-sweep")
+    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "sweep", "all"],
+                    help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
+                         "3/4/5: only that config; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
     args = ap.parse_args()
@@ -362,7 +362,7 @@ def main():
     }
     del plan, x, y
     torch.cuda.empty_cache()
-    if args.config in ("2", "all"):
+    if args.config in ("default", "all"):
         result["config3"] = cfg3(10, 3)
         torch.cuda.empty_cache()
         result["config4"] = cfg4(20, 5)
