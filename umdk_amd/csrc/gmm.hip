@@ -47,27 +47,30 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
 constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
-constexpr int GTHREADS = 256;        // 4 waves
+constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
 constexpr int G_MAX_NK = 256;        // fp8 k <= 32768
 
 // Tile shapes.  BM = 128: 2 x 2 waves of 64 x 128, 3-stage ring (prefill: many rows per expert).
 // BM = 32: 1 x 4 waves of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the
 // k-loop is a weight stream and the extra stage keeps more of it in flight).
+// BM = 256 (bf16 only): 8 waves, 2 x 4 of 128 x 64 (two waves per SIMD hide each other's LDS reads),
+// a 2-stage ring -- half the L2->LDS bytes per FLOP of the 128-row tile, for compute-bound prefill.
 template <int BM_> struct Tile {
     static constexpr int BM = BM_;
+    static constexpr int NWAVES = BM >= 256 ? 8 : 4;
+    static constexpr int THREADS = 64 * NWAVES;
     static constexpr int WAVES_M = BM >= 128 ? 2 : 1;
-    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int WAVES_N = NWAVES / WAVES_M;
     static constexpr int WM = BM / WAVES_M, WN = GBN / WAVES_N;  // wave tile
     static constexpr int IF = WM / 16, JF = WN / 16;              // MFMA fragments per wave
-    static constexpr int STAGES = BM >= 128 ? 3 : 4;
+    static constexpr int STAGES = BM >= 256 ? 2 : BM >= 128 ? 3 : 4;
     static constexpr int A_BYTES = BM * GKB;
     static constexpr int B_BYTES = GBN * GKB;
-    static constexpr int S_BYTES = 4 * 64 * 4;   // per-wave copies of 64 activation scales
+    static constexpr int S_BYTES = NWAVES * 64 * 4;  // per-wave copies of 64 activation scales
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES + S_BYTES;
-    static constexpr int A_LOADS = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage (1 KiB each)
-    static constexpr int B_LOADS = B_BYTES / 1024 / 4;
-    static_assert(WM <= 64, "one 64-lane scale DMA per wave covers its rows");
+    static constexpr int A_LOADS = A_BYTES / 1024 / NWAVES;  // DMA instructions per wave per stage (1 KiB each)
+    static constexpr int B_LOADS = B_BYTES / 1024 / NWAVES;
 };
 
 struct GroupTable {
@@ -76,7 +79,7 @@ struct GroupTable {
 };
 
 // Block-wide exclusive scans of ceil(cnt/GBM) and cnt over the L experts.
-template <int GBM>
+template <int GBM, int GTHREADS>
 __device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch)
 {
     const int tid = threadIdx.x;
@@ -146,18 +149,20 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
 }
 
 template <int DT, int EPI, int BM>
-__global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
+__global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
 {
     using TC = Tile<BM>;
+    constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
+    static_assert(DT == DT_BF16 || TC::WM <= 64, "fp8 tiles: one 64-lane scale DMA per wave, VALU accumulators");
     constexpr int GBM = TC::BM, WM = TC::WM, WN = TC::WN, IF = TC::IF, JF = TC::JF;
     constexpr int GSTAGES = TC::STAGES, STAGE_BYTES = TC::STAGE_BYTES;
     constexpr int A_BYTES = TC::A_BYTES, B_BYTES = TC::B_BYTES, A_LOADS = TC::A_LOADS, B_LOADS = TC::B_LOADS;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
-    int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GTHREADS ints: table scan, then the fp8 amax exchange
-    float *wsc = reinterpret_cast<float *>(scratch + 2 * GTHREADS);  // [2][G_MAX_NK] weight scales of the tile
+    int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GMAX_THREADS ints: table scan, then the fp8 amax exchange
+    float *wsc = reinterpret_cast<float *>(scratch + 2 * GMAX_THREADS);  // [2][G_MAX_NK] weight scales of the tile
 
-    build_group_table<GBM>(p.group_list, p.L, *gt, scratch);
+    build_group_table<GBM, GTHREADS>(p.group_list, p.L, *gt, scratch);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -208,12 +213,12 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
         uint32_t ga[A_LOADS], gb[B_LOADS];
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int r = (i * 4 + w) * 8 + band_row;  // tile row 0..GBM-1
+            const int r = (i * NW + w) * 8 + band_row;  // tile row 0..GBM-1
             ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off;
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
-            const int r = (i * 4 + w) * 8 + band_row;  // LDS W row 0..255
+            const int r = (i * NW + w) * 8 + band_row;  // LDS W row 0..255
             int wrow;
             if (SWIGLU) {
                 // LDS rows [WN c, WN c + WN) feed column wave c: WN/2 gate rows, then the
@@ -234,10 +239,10 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
             uint8_t *st = smem + slot * STAGE_BYTES;
 #pragma unroll
             for (int i = 0; i < A_LOADS; ++i)
-                dma16(p.A + ga[i] + (uint32_t)kc * GKB, st + (i * 4 + w) * 1024);
+                dma16(p.A + ga[i] + (uint32_t)kc * GKB, st + (i * NW + w) * 1024);
 #pragma unroll
             for (int i = 0; i < B_LOADS; ++i)
-                dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * 4 + w) * 1024);
+                dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
             if constexpr (FP8)
                 dma4(p.As + gs + kc, st + A_BYTES + B_BYTES + w * 256);
         };
@@ -417,15 +422,15 @@ __global__ __launch_bounds__(GTHREADS, 1) void gmm_kernel(GmmArgs p)
     }
 }
 
-template <int BM> static size_t lds_bytes()
+template <int BM> constexpr size_t lds_bytes()
 {
-    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GTHREADS * sizeof(int) +
+    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int) +
            2 * G_MAX_NK * sizeof(float);
 }
-static_assert(sizeof(GroupTable) + 2 * GTHREADS * 4 + 2 * G_MAX_NK * 4 + 3 * Tile<128>::STAGE_BYTES <= 163840, "LDS");
-static_assert(sizeof(GroupTable) + 2 * GTHREADS * 4 + 2 * G_MAX_NK * 4 + 4 * Tile<32>::STAGE_BYTES <= 163840, "LDS");
+static_assert(lds_bytes<32>() <= 163840 && lds_bytes<128>() <= 163840 && lds_bytes<256>() <= 163840,
+              "LDS budget of a gfx950 workgroup");
 
-size_t gmm_lds_bytes() { return lds_bytes<128>() > lds_bytes<32>() ? lds_bytes<128>() : lds_bytes<32>(); }
+size_t gmm_lds_bytes() { return lds_bytes<128>() > lds_bytes<32>() ? lds_bytes<128>() : lds_bytes<32>(); }  // upper bound
 
 static int g_num_cus = 0;
 
@@ -449,7 +454,7 @@ template <int DT, int EPI, int BM> static hipError_t launch_bm(const GmmArgs &a,
             g_num_cus = 256;
     }
     const int grid = (g_num_cus + 7) / 8 * 8;
-    hipLaunchKernelGGL((gmm_kernel<DT, EPI, BM>), dim3(grid), dim3(GTHREADS), lds, s, a);
+    hipLaunchKernelGGL((gmm_kernel<DT, EPI, BM>), dim3(grid), dim3(Tile<BM>::THREADS), lds, s, a);
     return hipGetLastError();
 }
 
@@ -459,6 +464,10 @@ template <int DT, int EPI> static hipError_t launch_one(const GmmArgs &a, hipStr
 {
     if (a.M <= 48 * a.L)
         return launch_bm<DT, EPI, 32>(a, s);
+    if constexpr (DT == DT_BF16) {
+        if (a.M >= 512 * a.L)
+            return launch_bm<DT, EPI, 256>(a, s);
+    }
     return launch_bm<DT, EPI, 128>(a, s);
 }
 
