@@ -49,7 +49,7 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
 constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
-constexpr int G_MAX_NK = 256;        // fp8 k <= 32768
+constexpr int G_MAX_NK = 128;        // fp8 k <= 16384
 
 // Tile shapes.  BM = 128: 2 x 2 waves of 64 x 128, 3-stage ring (prefill: many rows per expert).
 // BM = 32: 1 x 4 waves of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the
@@ -58,7 +58,7 @@ constexpr int G_MAX_NK = 256;        // fp8 k <= 32768
 // a 2-stage ring -- half the L2->LDS bytes per FLOP of the 128-row tile, for compute-bound prefill.
 template <int BM_> struct Tile {
     static constexpr int BM = BM_;
-    static constexpr int NWAVES = BM >= 256 ? 8 : 4;
+    static constexpr int NWAVES = BM >= 128 ? 8 : 4;
     static constexpr int THREADS = 64 * NWAVES;
     static constexpr int WAVES_M = BM >= 128 ? 2 : 1;
     static constexpr int WAVES_N = NWAVES / WAVES_M;
