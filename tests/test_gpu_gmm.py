@@ -165,3 +165,45 @@ def test_gmm_rejects_bad_shapes(ops):
     gl = torch.tensor([8], dtype=torch.int64, device="cuda")
     with pytest.raises(Exception, match="multiple of"):
         ops.grouped_matmul(x, None, gl, w, None)
+
+
+def _ragged_vs_torch(ops, counts, H, I, dtype, spare, seed):
+    """GMM1+SwiGLU then GMM2 on x with `spare` rows past the groups, against an fp32 torch reference."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    L, M = len(counts), sum(counts)
+    x = torch.randn(M + spare, H, device="cuda", generator=g)
+    w1 = torch.randn(L, 2 * I, H, device="cuda", generator=g) * 0.02
+    w2 = torch.randn(L, H, I, device="cuda", generator=g) * 0.02
+    gl = torch.tensor(counts, dtype=torch.int64, device="cuda")
+    if dtype == "bf16":
+        xb, w1b, w2b = x.bfloat16(), w1.bfloat16(), w2.bfloat16()
+        h, _ = ops.grouped_matmul_swiglu(xb, None, gl, w1b, None, 0)
+        out = ops.grouped_matmul(h, None, gl, w2b, None)
+        rh, ro = _torch_ffn(xb, counts, w1b, w2b, I)
+        hg, tol = h.float(), 2e-2
+    else:
+        xq, xs = fp8_quant_rows(x)
+        w1q, w1s = fp8_quant_weight(w1)
+        w2q, w2s = fp8_quant_weight(w2)
+        h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1q, w1s, 3)
+        out = ops.grouped_matmul(h, hs, gl, w2q, w2s)
+        w1d = (w1q.float().view(L, 2 * I // 128, 128, H // 128, 128) * w1s[:, :, None, :, None]).view(L, 2 * I, H)
+        w2d = (w2q.float().view(L, H // 128, 128, I // 128, 128) * w2s[:, :, None, :, None]).view(L, H, I)
+        rh, _ = _torch_ffn(dq_rows(xq, xs), counts, w1d, w2d, I)
+        hd = dq_rows(h, hs)[:M]
+        ro = torch.cat([hd[sum(counts[:e]):sum(counts[:e + 1])] @ w2d[e].T for e in range(L)])
+        hg, tol = dq_rows(h, hs), 5e-2
+    assert relerr(hg[:M], rh) < tol
+    assert relerr(out[:M].float(), ro) < tol
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_long_segments_take_256_row_tile(ops, dtype):
+    # >= 512 rows per touched expert selects the 256-row tile on the device
+    _ragged_vs_torch(ops, [700, 0, 1100, 520], 2048, 512, dtype, 5, 21)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_short_segments_in_large_capacity_take_128_row_tile(ops, dtype):
+    # a 4096-row capacity (prefill-sized) holding 45 rows: the device picks the 128-row tile over the 256-row one
+    _ragged_vs_torch(ops, [10, 0, 30, 5], 1024, 256, dtype, 4096 - 45, 22)

@@ -20,6 +20,7 @@ struct GmmArgs {
     const float *Ws;            // fp8: [L, N/128, K/128]
     uint8_t *C;                 // plain: bf16 [M, N]; SwiGLU: h [M, N/2] (bf16 or fp8)
     float *Cs;                  // SwiGLU fp8: [M, N/256] h block scales
+    int allow256 = 1;           // set by the launcher: the 256-row tile may be picked on the device
 };
 
 size_t gmm_lds_bytes();

@@ -67,7 +67,9 @@ template <int BM_> struct Tile {
     static constexpr int STAGES = BM >= 256 ? 2 : BM >= 128 ? 3 : 4;
     static constexpr int A_BYTES = BM * GKB;
     static constexpr int B_BYTES = GBN * GKB;
-    static constexpr int S_BYTES = NWAVES * 64 * 4;  // per-wave copies of 64 activation scales
+    static constexpr int S_ROWS = WM > 64 ? WM : 64;  // activation-scale rows a wave DMAs (64 per instruction)
+    static constexpr int S_DMAS = S_ROWS / 64;
+    static constexpr int S_BYTES = NWAVES * S_ROWS * 4;  // per-wave copies of its rows' activation scales
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES + S_BYTES;
     static constexpr int A_LOADS = A_BYTES / 1024 / NWAVES;  // DMA instructions per wave per stage (1 KiB each)
     static constexpr int B_LOADS = B_BYTES / 1024 / NWAVES;
@@ -148,12 +150,10 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
 }
 
-template <int DT, int EPI, int BM>
-__global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
+template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p)
 {
     using TC = Tile<BM>;
     constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
-    static_assert(DT == DT_BF16 || TC::WM <= 64, "fp8 tiles: one 64-lane scale DMA per wave, VALU accumulators");
     constexpr int GBM = TC::BM, WM = TC::WM, WN = TC::WN, IF = TC::IF, JF = TC::JF;
     constexpr int GSTAGES = TC::STAGES, STAGE_BYTES = TC::STAGE_BYTES;
     constexpr int A_BYTES = TC::A_BYTES, B_BYTES = TC::B_BYTES, A_LOADS = TC::A_LOADS, B_LOADS = TC::B_LOADS;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
     constexpr bool FP8 = DT == DT_FP8;
-    constexpr int LOADS = A_LOADS + B_LOADS + (FP8 ? 1 : 0);  // DMA instructions per wave per stage
+    constexpr int LOADS = A_LOADS + B_LOADS + (FP8 ? TC::S_DMAS : 0);  // DMA instructions per wave per stage
     const int esz = FP8 ? 1 : 2;
     const uint32_t kbytes = (uint32_t)p.K * esz;  // bytes per row
     const int nk = (int)(kbytes / GKB);
@@ -231,8 +231,11 @@ __global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
             }
             gb[i] = (uint32_t)wrow * kbytes + chunk_off;
         }
-        // fp8: this wave's activation-scale rows (the WM rows of its row block wm; 64 lanes)
-        const uint32_t gs = (uint32_t)min(row0 + wm * WM + lane, p.M - 1) * (uint32_t)nk;
+        // fp8: this wave's activation-scale rows (the WM rows of its row block wm, 64 per DMA)
+        uint32_t gs[TC::S_DMAS];
+#pragma unroll
+        for (int d = 0; d < TC::S_DMAS; ++d)
+            gs[d] = (uint32_t)min(row0 + wm * WM + d * 64 + lane, p.M - 1) * (uint32_t)nk;
 
         auto issue = [&](int ks, int slot) {
             const int kc = min(ks, nk - 1);  // past the end: reload the last k-step (keeps the count uniform)
@@ -243,8 +246,11 @@ __global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
 #pragma unroll
             for (int i = 0; i < B_LOADS; ++i)
                 dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
-            if constexpr (FP8)
-                dma4(p.As + gs + kc, st + A_BYTES + B_BYTES + w * 256);
+            if constexpr (FP8) {
+#pragma unroll
+                for (int d = 0; d < TC::S_DMAS; ++d)
+                    dma4(p.As + gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            }
         };
 
         f32x4 acc[IF][JF];
@@ -296,33 +302,32 @@ __global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
                     }
                 }
             } else {
-                const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * 256);
+                const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4);
                 const float sg = ws_g[ks];
                 const float su = SWIGLU ? ws_u[ks] : sg;
-                float sa[IF];
-                i32x8 afr[IF];
-#pragma unroll
-                for (int i = 0; i < IF; ++i) {
-                    sa[i] = sst[i * 16 + l16];
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
-                    afr[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                   (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                }
+                // all W fragments of the wave are held; A fragments stream one at a time
+                i32x8 bfr[JF];
 #pragma unroll
                 for (int j = 0; j < JF; ++j) {
                     const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg));
                     const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg + 1));
-                    const i32x8 bfr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                            (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                    // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
-                    const float sw = (SWIGLU && j >= JF / 2) ? su : sg;
+                    bfr[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                   (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                }
 #pragma unroll
-                    for (int i = 0; i < IF; ++i) {
+                for (int i = 0; i < IF; ++i) {
+                    const float sa = sst[i * 16 + l16];
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
+                    const i32x8 afr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                            (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+#pragma unroll
+                    for (int j = 0; j < JF; ++j) {
                         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                         const f32x4 d =
-                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr, afr[i], z, 0, 0, 0, 127, 0, 127);
-                        const float s = sa[i] * sw;
+                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr[j], afr, z, 0, 0, 0, 127, 0, 127);
+                        // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
+                        const float s = sa * ((SWIGLU && j >= JF / 2) ? su : sg);
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
                             acc[i][j][q] += d[q] * s;
@@ -422,6 +427,42 @@ __global__ __launch_bounds__(Tile<BM>::THREADS, 1) void gmm_kernel(GmmArgs p)
     }
 }
 
+// Decode-sized segments: the 32-row tile (4 waves).
+template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_small(GmmArgs p)
+{
+    gmm_body<DT, EPI, 32>(p);
+}
+
+// Prefill: 8 waves, 128- or 256-row tile picked per launch from the actual rows per touched
+// expert (counts are on the device).  The choice is block-uniform and identical in every block.
+template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
+{
+    // the first bytes of the dynamic LDS serve as the reduction slots before the tile body starts
+    // (a static __shared__ array would push the 1 KiB-aligned dynamic region past the LDS limit)
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    int *red = reinterpret_cast<int *>(smem);
+    if (threadIdx.x < 2)
+        red[threadIdx.x] = 0;
+    __syncthreads();
+    int rows = 0, touched = 0;
+    for (int e = threadIdx.x; e < p.L; e += blockDim.x) {
+        const int c = (int)p.group_list[e];
+        rows += c;
+        touched += c > 0;
+    }
+    if (rows)
+        atomicAdd(&red[0], rows);
+    if (touched)
+        atomicAdd(&red[1], touched);
+    __syncthreads();
+    const int r = red[0] / (red[1] > 0 ? red[1] : 1);
+    __syncthreads();
+    if (p.allow256 && r >= 512)
+        gmm_body<DT, EPI, 256>(p);
+    else
+        gmm_body<DT, EPI, 128>(p);
+}
+
 template <int BM> constexpr size_t lds_bytes()
 {
     return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int) +
@@ -434,41 +475,51 @@ size_t gmm_lds_bytes() { return lds_bytes<128>() > lds_bytes<32>() ? lds_bytes<1
 
 static int g_num_cus = 0;
 
-template <int DT, int EPI, int BM> static hipError_t launch_bm(const GmmArgs &a, hipStream_t s)
+static int num_cus()
 {
-    static bool attr_set = false;
-    const size_t lds = lds_bytes<BM>();
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)gmm_kernel<DT, EPI, BM>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
     if (g_num_cus == 0) {
-        int dev = 0;
+        int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&g_num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            g_num_cus = 0;
-        if (g_num_cus <= 0)
-            g_num_cus = 256;
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        g_num_cus = n;
     }
-    const int grid = (g_num_cus + 7) / 8 * 8;
-    hipLaunchKernelGGL((gmm_kernel<DT, EPI, BM>), dim3(grid), dim3(Tile<BM>::THREADS), lds, s, a);
-    return hipGetLastError();
+    return g_num_cus;
 }
 
-// Tile choice from the row capacity per expert: segments of a few rows (decode) get the 32-row
-// tile, whose k-loop is nearly all weight bytes.
-template <int DT, int EPI> static hipError_t launch_one(const GmmArgs &a, hipStream_t s)
+template <typename K> static hipError_t set_lds(K kernel, size_t lds, bool &done)
 {
-    if (a.M <= 48 * a.L)
-        return launch_bm<DT, EPI, 32>(a, s);
-    if constexpr (DT == DT_BF16) {
-        if (a.M >= 512 * a.L)
-            return launch_bm<DT, EPI, 256>(a, s);
+    if (done)
+        return hipSuccess;
+    hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    done = e == hipSuccess;
+    return e;
+}
+
+// Tile choice.  A row capacity of at most 48 rows per expert (decode) can only hold short
+// segments: the 32-row kernel.  Otherwise the 8-wave kernel, which picks the 128- or 256-row
+// tile on the device from the actual counts (a prefill-sized capacity may still hold short
+// segments when most rows are routed elsewhere).  One launch, no host synchronisation.
+template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s)
+{
+    const int grid = (num_cus() + 7) / 8 * 8;
+    if (a.M <= 48 * a.L) {
+        static bool done = false;
+        const size_t lds = lds_bytes<32>();
+        hipError_t e = set_lds(gmm_kernel_small<DT, EPI>, lds, done);
+        if (e != hipSuccess)
+            return e;
+        hipLaunchKernelGGL((gmm_kernel_small<DT, EPI>), dim3(grid), dim3(256), lds, s, a);
+        return hipGetLastError();
     }
-    return launch_bm<DT, EPI, 128>(a, s);
+    a.allow256 = a.M >= 512 * a.L;
+    static bool done = false;
+    const size_t lds = lds_bytes<128>() > lds_bytes<256>() ? lds_bytes<128>() : lds_bytes<256>();
+    hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, done);
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL((gmm_kernel_big<DT, EPI>), dim3(grid), dim3(512), lds, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
