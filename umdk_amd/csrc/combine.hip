@@ -104,6 +104,22 @@ __global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
     }
 }
 
+hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                                 const float *topk_w, int T, int K, int H, uint16_t *out, const int32_t *inv,
+                                 hipStream_t s)
+{
+    if (T == 0)
+        return hipSuccess;
+    if (H > COMB_NIT * 1024 || (H & 15) || K > 64)
+        return hipErrorInvalidValue;
+    const int nchunk = (H + 1023) / 1024;
+    const long items = (long)T * nchunk;
+    hipLaunchKernelGGL(combine_gather_kernel, dim3((unsigned)((items + COMB_WAVES - 1) / COMB_WAVES)),
+                       dim3(COMB_WAVES * 64), 0, s, y, expand_idx, N, recv_count_last, topk_w, T, K, H, nchunk, out,
+                       inv);
+    return hipGetLastError();
+}
+
 hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
                           const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *inv_ws, hipStream_t s)
 {

@@ -49,7 +49,8 @@ template <int MODE>
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
     const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap, int nchunk,
-    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx)
+    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
+    int32_t *__restrict__ inv_out)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -58,6 +59,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
         return;
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
     const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
+    if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
+        inv_out[(size_t)t * K + lane] = dst;
     if constexpr (MODE == QUANT_NONE) {
         // lane l copies columns [1024 j + 8 l, +8) and [1024 j + 512 + 8 l, +8): each 16-byte
         // store instruction of the wave writes one contiguous kilobyte
@@ -133,7 +136,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
     const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap,
-    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx)
+    uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
+    int32_t *__restrict__ inv_out)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -141,6 +145,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     if (t >= T)
         return;
     const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
+    if (inv_out && lane < K)
+        inv_out[(size_t)t * K + lane] = dst;
     const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)t * H);
     u32x4 raw[DISP_NIT][2];
 #pragma unroll
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
-                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s)
+                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out)
 {
     if (T == 0)
         return hipSuccess;
@@ -221,17 +227,17 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
     switch (quant_mode) {
     case QUANT_NONE:
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_NONE>, grid_chunk, block, 0, s, x, topk_idx, send_offset,
-                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx);
+                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out);
         break;
     case QUANT_INT8_TOKEN:
         hipLaunchKernelGGL(dispatch_int8_kernel, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x, topk_idx,
-                           send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx);
+                           send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx, inv_out);
         break;
     case QUANT_FP8_BLOCK:
         if (H & 127)
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_FP8_BLOCK>, grid_chunk, block, 0, s, x, topk_idx,
-                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx);
+                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out);
         break;
     default:
         return hipErrorInvalidValue;

@@ -3,7 +3,9 @@
 // fused_deep_moe.h:355-448) on one GPU, composed from the path's kernels:
 //   prepare ids (x_active_mask, local expert range) -> layout -> count
 //   exchange -> quantised dispatch -> GMM1+SwiGLU -> GMM2 -> combine,
-//   plus the optional shared expert on all tokens.
+//   plus the optional shared expert on all tokens.  At decode sizes
+//   (batch*topk <= 8192) the first three stages are one single-block launch,
+//   and dispatch writes the combine's row map: five launches in all.
 // Every intermediate lives in the caller's workspace and every size is fixed
 // by (batch, topk): no host synchronisation and no allocation, so the call can
 // be captured in a HIP graph (the reference's fused op is its graph-capturable
@@ -121,6 +123,8 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             "fused_deep_moe: hidden %lld must be in [1024,7168] and a multiple of 256", (long long)hidden);
     F_CHECK(gmm1HiddenSize >= 256 && gmm1HiddenSize % 256 == 0,
             "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
+    F_CHECK(weightDtype != CAMHIP_DTYPE_FP8 || (gmm1HiddenSize / 2 <= 16384 && shareGmm1HiddenSize / 2 <= 16384),
+            "fused_deep_moe: fp8 intermediate sizes above 16384 are not supported");
     F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_FP8,
             "fused_deep_moe: weight dtype %lld not supported (bf16 or fp8 e4m3fn)", (long long)weightDtype);
     F_CHECK(quantMode == 0, "fused_deep_moe: quant_mode is reserved and must be 0 (got %lld)", (long long)quantMode);
@@ -174,20 +178,28 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         if (T == 0) {  // no tokens: no expert receives any
             return cam::launch_fill_i64(expertTokenNums, 0, L, s);
         }
-        HIP_TRY(cam::launch_prepare_ids(expertIds, xActiveMask, T, K, 0, L, ids, s));
-        HIP_TRY(cam::launch_layout_i32(ids, T, K, L, counts, (int32_t *)P(f.sti), P(f.layout_ws), s));
-        HIP_TRY(cam::launch_notify(counts, L, T, send_off, (int32_t *)P(f.total), recv_cnt, nullptr, nullptr,
-                                   expertTokenNums, L, s));
+        if (N <= 8192) {
+            // decode sizes: id preparation, layout and count exchange in one launch
+            HIP_TRY(cam::launch_layout_small(expertIds, xActiveMask, T, K, L, ids, counts, (int32_t *)P(f.sti),
+                                             send_off, recv_cnt, (int32_t *)P(f.total), expertTokenNums, s));
+        } else {
+            HIP_TRY(cam::launch_prepare_ids(expertIds, xActiveMask, T, K, 0, L, ids, s));
+            HIP_TRY(cam::launch_layout_i32(ids, T, K, L, counts, (int32_t *)P(f.sti), P(f.layout_ws), s));
+            HIP_TRY(cam::launch_notify(counts, L, T, send_off, (int32_t *)P(f.total), recv_cnt, nullptr, nullptr,
+                                       expertTokenNums, L, s));
+        }
+        // dispatch also writes the combine's row map (inv), so the combine is a single gather
         HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
-                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s));
+                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv)));
         cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
                         (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
         HIP_TRY(cam::launch_gmm(g1, dt, epi1, s));
         cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
                         (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
         HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
-        HIP_TRY(cam::launch_combine((const uint16_t *)P(f.y), (const int32_t *)P(f.eidx), N, recv_cnt + (L - 1),
-                                    expertScales, T, K, H, output, (int32_t *)P(f.inv), s));
+        HIP_TRY(cam::launch_combine_gather((const uint16_t *)P(f.y), (const int32_t *)P(f.eidx), N,
+                                           recv_cnt + (L - 1), expertScales, T, K, H, output,
+                                           (const int32_t *)P(f.inv), s));
         if (shared) {
             // shared expert on every token: x quantised in token order, one group of T rows
             int64_t *gl = (int64_t *)P(f.sh_gl);

@@ -26,6 +26,11 @@ hipError_t launch_layout(const int64_t *topk_idx, int T, int K, int E, int R, in
 hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
                              int32_t *send_token_idx, void *ws, hipStream_t s);
 
+// decode-sized layout + count exchange in one launch (T*K <= 8192; ids masked by `active`)
+hipError_t launch_layout_small(const int32_t *ids, const uint8_t *active, int T, int K, int E, int32_t *ids_eff,
+                               int32_t *counts, int32_t *sti, int32_t *send_offset, int32_t *recv_count,
+                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s);
+
 // ---- small utilities (notify.hip)
 hipError_t launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t s);
 
@@ -37,7 +42,12 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
 // ---- permute + quantise (dispatch.hip); topk_idx == nullptr: identity rows (K must be 1)
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
-                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s);
+                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
+                           int32_t *inv_out = nullptr);
+// combine without the scatter launch, for callers whose dispatch already wrote inv
+hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                                 const float *topk_w, int T, int K, int H, uint16_t *out, const int32_t *inv,
+                                 hipStream_t s);
 
 // ---- fused decode helpers (fused.hip)
 hipError_t launch_prepare_ids(const int32_t *ids, const uint8_t *active, int T, int K, int first_local, int L,

@@ -218,3 +218,110 @@ hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32
 }
 
 }  // namespace cam
+
+namespace cam {
+
+// Decode-sized fused bookkeeping (T*K <= 8192 entries): one block of 1024 threads does what
+// prepare_ids + the three layout launches + the count exchange do for the prefill path:
+//   ids_eff[t,k] = expert id if the token is active and the id is in [0,E), else -1;
+//   send_token_idx = stable rank within the expert (same ballot ranking as layout_rank_kernel,
+//   1024 entries per round, rounds in order); counts, exclusive offsets, inclusive recv_count,
+//   int64 tokens per expert and the total.
+constexpr int SMALL_THREADS = 1024;
+constexpr int SMALL_WAVES = SMALL_THREADS / 64;
+
+__global__ __launch_bounds__(SMALL_THREADS) void layout_small_kernel(
+    const int32_t *__restrict__ ids, const uint8_t *__restrict__ active, int T, int K, int E,
+    int32_t *__restrict__ ids_eff, int32_t *__restrict__ counts, int32_t *__restrict__ sti,
+    int32_t *__restrict__ send_offset, int32_t *__restrict__ recv_count, int32_t *__restrict__ total,
+    int64_t *__restrict__ tokens_per_expert)
+{
+    __shared__ int32_t run[MAX_E];
+    __shared__ int32_t wave_hist[SMALL_WAVES][MAX_E];
+    __shared__ int32_t wsum[SMALL_WAVES];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int TK = T * K;
+    for (int e = tid; e < E; e += SMALL_THREADS)
+        run[e] = 0;
+    const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+    const uint64_t lt = lanemask_lt();
+    for (int base = 0; base < TK; base += SMALL_THREADS) {
+        for (int j = tid; j < SMALL_WAVES * E; j += SMALL_THREADS)
+            wave_hist[j / E][j % E] = 0;
+        __syncthreads();
+        const int i = base + tid;
+        int e = -1;
+        if (i < TK) {
+            const int id = ids[i];
+            const bool on = (active == nullptr || active[i / K] != 0) && id >= 0 && id < E;
+            e = on ? id : -1;
+            ids_eff[i] = e;
+        }
+        const bool valid = e >= 0;
+        uint64_t peers = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const int inrank = __popcll(peers & lt);
+        if (valid && inrank == 0)
+            wave_hist[w][e] = __popcll(peers);
+        __syncthreads();
+        if (i < TK) {
+            int32_t r = -1;
+            if (valid) {
+                r = run[e] + inrank;
+                for (int ww = 0; ww < w; ++ww)
+                    r += wave_hist[ww][e];
+            }
+            sti[i] = r;
+        }
+        __syncthreads();
+        for (int ee = tid; ee < E; ee += SMALL_THREADS) {
+            int32_t sacc = 0;
+#pragma unroll
+            for (int ww = 0; ww < SMALL_WAVES; ++ww)
+                sacc += wave_hist[ww][ee];
+            run[ee] += sacc;
+        }
+        __syncthreads();
+    }
+    // count exchange of one rank: exclusive / inclusive prefix over the experts
+    const int c = tid < E ? run[tid] : 0;
+    int32_t v = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int32_t u = __shfl_up(v, o, 64);
+        if (lane >= o)
+            v += u;
+    }
+    if (lane == 63)
+        wsum[w] = v;
+    __syncthreads();
+    int32_t before = 0;
+    for (int ww = 0; ww < w; ++ww)
+        before += wsum[ww];
+    const int32_t incl = before + v;
+    if (tid < E) {
+        counts[tid] = c;
+        send_offset[tid] = incl - c;
+        recv_count[tid] = incl;
+        tokens_per_expert[tid] = c;
+        if (tid == E - 1)
+            *total = incl;
+    }
+}
+
+hipError_t launch_layout_small(const int32_t *ids, const uint8_t *active, int T, int K, int E, int32_t *ids_eff,
+                               int32_t *counts, int32_t *sti, int32_t *send_offset, int32_t *recv_count,
+                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s)
+{
+    if (T * K > 8192 || E > MAX_E || E > SMALL_THREADS)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(layout_small_kernel, dim3(1), dim3(SMALL_THREADS), 0, s, ids, active, T, K, E, ids_eff, counts,
+                       sti, send_offset, recv_count, total, tokens_per_expert);
+    return hipGetLastError();
+}
+
+}  // namespace cam

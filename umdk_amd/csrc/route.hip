@@ -61,16 +61,22 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
     const bool live = t < T;  // dead rows still run the DPP steps (they read only their own row)
     const float *l = logits + (size_t)(live ? t : 0) * E;
     uint32_t khi[PER];
+    float lg[PER], bs[PER];
+    // loads first, all unconditional (clamped index) so they are in flight together
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = min(l16 + 16 * j, E - 1);
+        lg[j] = l[e];
+        bs[j] = bias ? bias[e] : 0.0f;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-        const int e = l16 + 16 * j;
-        khi[j] = 0;
-        if (e < E && live) {
-            const float lg = l[e];
-            mx = fmaxf(mx, lg);
-            khi[j] = order_key(bias ? lg + bias[e] : lg);
-        }
+        const bool valid = live && l16 + 16 * j < E;
+        // + 0.0f turns -0.0 into +0.0, so the integer key orders zeros as a float compare does
+        const float sc = (bias ? lg[j] + bs[j] : lg[j]) + 0.0f;
+        mx = valid ? fmaxf(mx, lg[j]) : mx;
+        khi[j] = valid ? order_key(sc) : 0u;
     }
     mx = fmax_step<DPP_QUAD_XOR1>(mx);
     mx = fmax_step<DPP_QUAD_XOR2>(mx);
