@@ -35,9 +35,10 @@
 //     epilogue stores 8 contiguous bytes per lane without a transpose.
 //   * fp8: one MFMA of K=128 per (i,j) per k-step covers exactly one scale
 //     block, so acc += mfma(...) * (a_scale[m] * w_scale[n-block]).
-//   * Persistent grid (one block per CU) walking tiles expert by expert,
-//     N-tile by N-tile, M-tiles fastest, remapped so that the blocks of one
-//     XCD take consecutive tiles (they share W tiles in that XCD's L2).
+//   * Persistent grid (one block per CU) walking tiles expert by expert in
+//     groups of 8 M-tiles x all N-tiles (M fastest), remapped so that the
+//     blocks of one XCD take consecutive tiles: they share A and W tiles in
+//     that XCD's L2.
 #include "cam_device.h"
 #include "gmm.h"
 
@@ -202,7 +203,13 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         const int e = __builtin_amdgcn_readfirstlane(lo);
         const int mt_e = __builtin_amdgcn_readfirstlane(gt->tile_prefix[e + 1] - gt->tile_prefix[e]);
         const int local = __builtin_amdgcn_readfirstlane(tile - gt->tile_prefix[e] * ntn);
-        const int nt = local / mt_e, mt = local % mt_e;
+        // within the expert: groups of up to 8 M-tiles, N-tiles in turn, the group's M-tiles
+        // fastest -- a run of consecutive tiles (one XCD's share of a round) covers ~8 A row blocks
+        // x a few W column blocks, so both operands are re-read from that XCD's L2
+        constexpr int GM = 8;
+        const int grp = local / (GM * ntn), rem = local % (GM * ntn);
+        const int gm = min(GM, mt_e - grp * GM);
+        const int nt = rem / gm, mt = grp * GM + rem % gm;
         const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
         const int seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
         const int row0 = seg0 + mt * GBM;
