@@ -158,14 +158,14 @@ def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
             "gemm_bound": "mfma" if (f1 + f2) / (peak * 1e12) > (ab1 + ab2) / (HBM_PEAK_GBPS * 1e9) else "hbm"}
 
 
-def gemm_sweep(steps, warmup, seed):
+def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536)):
     """fp8 GMM1+GMM2 at DeepSeek-V3 expert shapes (32 experts, H=7168, I=2048) for growing M."""
     from umdk_amd import ops
     dev = torch.device("cuda:0")
     H, I, L = 7168, 2048, 32
     w1, s1, w2, s2 = make_weights(L, H, I, "fp8", dev, seed)
     out = []
-    for M in (4096, 8192, 16384, 32768, 65536):
+    for M in ms:
         gl = torch.full((L,), M // L, dtype=torch.int64, device=dev)
         xq = (torch.randn(M, H, device=dev) * 0.5).to(torch.float8_e4m3fn)
         xs = torch.full((M, H // 128), 0.01, device=dev)
@@ -261,6 +261,7 @@ def main():
     ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "sweep", "all"],
                     help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
                          "3/4/5: only that config; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
+    ap.add_argument("--sweep-m", type=int, default=0, help="--config sweep: only this M")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
     args = ap.parse_args()
@@ -287,7 +288,9 @@ def main():
     if args.config in ("3", "4", "5", "sweep"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed),
-             "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed)}[args.config]()
+             "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
+                                         (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536))
+             }[args.config]()
         print(json.dumps({"config": args.config, "result": r}))
         return
 

@@ -27,7 +27,7 @@
 //     scales of the k-step ride the same DMA (4-byte lanes).  A wave's loads
 //     are counted with s_waitcnt vmcnt and published with a bare s_barrier
 //     (no fence, so outstanding prefetches are not drained).
-//   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row & 7):
+//   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row >> 1) & 7:
 //     each lane fetches the global chunk that belongs at its DMA slot, so
 //     fragment reads spread over all banks.
 //   * MFMA operands are (W fragment, A fragment), so a lane's four
@@ -126,7 +126,10 @@ __device__ void build_group_table(const int64_t *__restrict__ group_list, int L,
     __syncthreads();
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * GKB + ((chunk ^ (row & 7)) << 4); }
+// LDS byte offset of 16-byte chunk `chunk` of row `row`.  Chunks are XOR-swizzled by (row >> 1) & 7:
+// two 128-byte rows share one 256-byte bank row, so the 16 rows of a fragment read (same logical
+// chunk) land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * GKB + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 // s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima)
 template <int N> __device__ __forceinline__ void wait_vmcnt()
@@ -184,9 +187,9 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     const int logical = (G & 7) ? (int)blockIdx.x : (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
 
     // DMA slot of this lane inside a 1 KiB band (8 rows x 128 B): row l/8, physical chunk l%8,
-    // which holds logical chunk (l%8) ^ (l/8)
+    // which holds logical chunk (l%8) ^ ((row >> 1) & 7) -- see swz()
     const int band_row = lane >> 3;
-    const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ band_row) << 4);
+    auto chunk_off = [&](int r) { return (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4); };
 
     for (int tile = logical; tile < total; tile += G) {
         // ---- tile -> (expert, n-tile, m-tile)
@@ -221,7 +224,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
             const int r = (i * NW + w) * 8 + band_row;  // tile row 0..GBM-1
-            ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off;
+            ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off(r);
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
@@ -236,7 +239,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             } else {
                 wrow = n0 + r;
             }
-            gb[i] = (uint32_t)wrow * kbytes + chunk_off;
+            gb[i] = (uint32_t)wrow * kbytes + chunk_off(r);
         }
         // fp8: this wave's activation-scale rows (the WM rows of its row block wm, 64 per DMA)
         uint32_t gs[TC::S_DMAS];
