@@ -152,17 +152,23 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  * (fused_deep_moe.h:56-238; kernels
  * grouped_matmul_slice_m_per_token_dequant_swiglu_quant_multistage_workspace.h:299-455 and
  * grouped_matmul_slice_m_per_token_dequant_multistage_workspace.h:141-292).  The
- * reference computes them in int8 only; these take bf16, or fp8 e4m3fn with
+ * reference computes them in int8 with per-channel weight and per-token
+ * activation scales; these take that int8 mode, bf16, or fp8 e4m3fn with
  * DeepSeek-style block scales.
  * x [m, k]: rows in dispatch order; expert g owns groupList[g] consecutive
  * rows starting at the sum of the earlier counts (groupList is int64 on the
  * device, as recvTokensPerExpert / expert_token_nums).  Rows past the sum are
  * neither read for output nor written.
  * weight [numGroups, n, k] with k contiguous (the transpose of the reference's
- * logical [L, k, n] layout).  dtype: CAMHIP_DTYPE_BF16 or CAMHIP_DTYPE_FP8;
- * for fp8, xScale [m, k/128] and weightScale [numGroups, n/128, k/128] fp32
- * (dequantised value = code * scale).  Accumulation is fp32. */
+ * logical [L, k, n] layout).  dtype: CAMHIP_DTYPE_BF16, CAMHIP_DTYPE_INT8 or
+ * CAMHIP_DTYPE_FP8; for fp8, xScale [m, k/128] and weightScale
+ * [numGroups, n/128, k/128] fp32 (dequantised value = code * scale),
+ * accumulation fp32; for int8, xScale [m] per token and weightScale
+ * [numGroups, n] per output channel, exact int32 accumulation and
+ * value = ((float)acc * weightScale[n]) * xScale[m]
+ * (block_epilogue_per_token_dequant.hpp:338-361). */
 #define CAMHIP_DTYPE_BF16 0
+#define CAMHIP_DTYPE_INT8 2
 #define CAMHIP_DTYPE_FP8 3
 
 /* GMM1 + SwiGLU: n = 2I, weight rows [0,I) gate, [I,2I) up;
@@ -170,7 +176,12 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  * (block_epilogue_per_token_dequant_swiglu.h:256-286).
  * outQuant CAMHIP_QUANT_NONE: h bf16; CAMHIP_QUANT_FP8_BLOCK: h fp8 e4m3fn with
  * hScale [m, I/128], quantised per 1x128 block like the dispatch quantiser.
- * Limits: 1 <= numGroups <= 512, k a multiple of 64 (bf16) / 128 (fp8),
+ * int8 inputs require outQuant CAMHIP_QUANT_INT8_TOKEN: h int8 [m, I] with
+ * hScale [m], requantised per token over the whole row,
+ * q = rint((h * 127) * (1/amax)), scale = amax * (1/127)
+ * (post_swiglu_dynamic_quant.h:164-231); this mode needs a workspace of
+ * m*I*4 + m*4 bytes (fp32 h and the row maxima), the others none.
+ * Limits: 1 <= numGroups <= 512, k a multiple of 64 (bf16) / 128 (fp8, int8),
  * I a multiple of 128, m*k and n*k bytes below 4 GiB. */
 CAMHIP_API camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(
     const void *x, const float *xScale, const int64_t *groupList, int64_t numGroups, int64_t m, int64_t k, int64_t n,
@@ -199,13 +210,18 @@ CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceS
  * fp32 combine weights; xActiveMask [batchSize] bool (1 byte, true prefix) or NULL.
  * Weights in coupled mode with the reduction dimension contiguous:
  * gmm1Weight [L, gmm1HiddenSize, hidden] (rows [0,I) gate, [I,2I) up),
- * gmm2Weight [L, hidden, gmm1HiddenSize/2]; weightDtype CAMHIP_DTYPE_BF16, or
+ * gmm2Weight [L, hidden, gmm1HiddenSize/2]; weightDtype CAMHIP_DTYPE_BF16,
  * CAMHIP_DTYPE_FP8 with block scales [L, n/128, k/128] (activations are then
- * quantised to fp8 1x128 on the fly).  The reference's int8 per-channel mode and
- * smooth-quant scales are not supported by this build (NULL required).
+ * quantised to fp8 1x128 on the fly), or CAMHIP_DTYPE_INT8, the reference's
+ * own mode: per-channel scales gmm1WeightScale [L, gmm1HiddenSize] and
+ * gmm2WeightScale [L, hidden], x quantised per token (s = 127/amax after the
+ * optional smooth scales expertSmoothScales [moeExpertNum, hidden] of the
+ * destination expert), h requantised per token between the GEMMs.  Smooth
+ * scales are accepted in int8 mode only (NULL otherwise).
  * Shared expert (optional, all four given together): shareGmm1Weight
  * [shareGmm1HiddenSize, hidden], shareGmm2Weight [hidden, shareGmm1HiddenSize/2]
- * (+ scales [n/128, k/128] for fp8) -> shareOutput [batchSize, hidden] bf16.
+ * (+ scales [n/128, k/128] for fp8, [n] for int8; int8 also takes
+ * shareSmoothScales [hidden]) -> shareOutput [batchSize, hidden] bf16.
  * Outputs: output [batchSize, hidden] bf16; expertTokenNums [L] int64 (rows per
  * local expert).  L = moeExpertNum / epRankSize; epRankSize must be 1 here.
  * quantMode is reserved (0), as in the reference.  Limits

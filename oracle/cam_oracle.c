@@ -33,6 +33,8 @@
  *                             (left half = gate through silu, right half = up),
  *                             post_swiglu_dynamic_quant.h:164-231 (requant of h).
  *   orc_gmm2_*             -- block_epilogue_per_token_dequant.hpp:338-361
+ *   orc_dispatch_int8_fused -- fused_deep_moe/.../raw_distributed/cam_moe_distribute_dispatch.h:640-681
+ *   orc_*_int8, orc_quant_rows_int8 -- the reference's own int8 W8A8 numerics (see their comment)
  *
  * Build with -ffp-contract=off: the combine and the quantisers are specified
  * as separate fp32 multiply and add steps, never a fused multiply-add.
@@ -261,6 +263,42 @@ ORC_API void orc_dispatch(const uint16_t *x, const int32_t *topk_idx, const int3
     free(bs);
 }
 
+/* Fused-op int8 dispatch (fused_deep_moe/.../cam_moe_distribute_dispatch.h:640-681; the shared
+ * expert's QuantToken in grouped_matmul_slice_m_per_token_dequant_swiglu_quant_multistage_workspace.h
+ * follows the same steps): f = float(x) [* smooth[e, h], e the destination expert], amax = max |f|,
+ * s = 127/amax (no epsilon), q = rint(f * s), scale = 1/s.  Each destination row is quantised on its
+ * own, since the smooth scales depend on the expert.  A zero row (amax 0) gets q = 0 and scale 0
+ * (the reference's 127/0 is undefined there). */
+ORC_API void orc_dispatch_int8_fused(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
+                                     const int32_t *send_token_idx, int T, int H, int K, int E, const float *smooth,
+                                     int8_t *expand_x, float *scales, int32_t *expand_idx)
+{
+    float *f = (float *)malloc(sizeof(float) * (size_t)H);
+    for (int t = 0; t < T; ++t) {
+        for (int k = 0; k < K; ++k) {
+            int e = topk_idx[(size_t)t * K + k];
+            if (e < 0 || e >= E)
+                continue;
+            size_t row = (size_t)send_offset[e] + (size_t)send_token_idx[(size_t)t * K + k];
+            float amax = 0.0f;
+            for (int h = 0; h < H; ++h) {
+                f[h] = bf16_to_f32(x[(size_t)t * H + h]);
+                if (smooth)
+                    f[h] = f[h] * smooth[(size_t)e * H + h];
+                amax = fabsf(f[h]) > amax ? fabsf(f[h]) : amax;
+            }
+            float s = amax > 0.0f ? 127.0f / amax : 0.0f;
+            for (int h = 0; h < H; ++h)
+                expand_x[row * H + h] = (int8_t)rintf(f[h] * s);
+            scales[row] = amax > 0.0f ? 1.0f / s : 0.0f;
+            expand_idx[row * 3 + 0] = 0;
+            expand_idx[row * 3 + 1] = t;
+            expand_idx[row * 3 + 2] = k;
+        }
+    }
+    free(f);
+}
+
 /* ------------------------------------------------------------------ C1 */
 
 /* y [N,H] bf16 in dispatch order, expand_idx [N,3], topk_idx/topk_w [T,K]
@@ -434,5 +472,77 @@ ORC_API void orc_gmm2_fp8(const uint8_t *Hq, const float *Hs, const int64_t *cnt
         }
     }
     free(a);
+    free(off);
+}
+
+/* ------------------------------------------------------------ int8 W8A8 (reference numerics) */
+/* The reference's fused path in int8: per-channel weight scales, per-token activation scales.
+ * GMM1 epilogue (block_epilogue_per_token_dequant_swiglu.h:256-286):
+ *   v = ((float)acc * w_scale[n]) * x_scale[m]; gate half through silu v / (1 + exp(-v)).
+ * Post-SwiGLU requant (post_swiglu_dynamic_quant.h:164-231), per token over the whole row:
+ *   h = silu(g) * u; amax = max |h|; q = rint((h * 127) * (1 / amax)); scale = amax * (1/127).
+ * GMM2 epilogue (block_epilogue_per_token_dequant.hpp:338-361):
+ *   out = bf16_rint(((float)acc * w_scale[n]) * h_scale[m]).
+ * Integer dot products are exact (int32). */
+ORC_API void orc_gmm1_swiglu_int8(const int8_t *A, const float *As, const int64_t *cnt, int L, const int8_t *W1,
+                                  const float *W1s, int H, int I, float *hout)
+{
+    int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
+    seg_offsets(cnt, L, off);
+    for (int e = 0; e < L; ++e) {
+        const int8_t *W = W1 + (size_t)e * 2 * I * H;
+        const float *Ws = W1s + (size_t)e * 2 * I;
+        for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            const int8_t *a = A + (size_t)m * H;
+            for (int i = 0; i < I; ++i) {
+                const int8_t *wg = W + (size_t)i * H, *wu = W + (size_t)(I + i) * H;
+                int32_t g = 0, u = 0;
+                for (int h = 0; h < H; ++h) {
+                    g += (int32_t)a[h] * (int32_t)wg[h];
+                    u += (int32_t)a[h] * (int32_t)wu[h];
+                }
+                float gf = ((float)g * Ws[i]) * As[m];
+                float uf = ((float)u * Ws[I + i]) * As[m];
+                gf = gf / (1.0f + expf(-gf));
+                hout[(size_t)m * I + i] = gf * uf;
+            }
+        }
+    }
+    free(off);
+}
+
+ORC_API void orc_quant_rows_int8(const float *h, int M, int I, int8_t *q, float *scale)
+{
+    for (int m = 0; m < M; ++m) {
+        const float *r = h + (size_t)m * I;
+        float amax = 0.0f;
+        for (int i = 0; i < I; ++i)
+            amax = fabsf(r[i]) > amax ? fabsf(r[i]) : amax;
+        const float inv = amax > 0.0f ? 1.0f / amax : 0.0f;  /* a zero row: q = 0, scale 0 */
+        for (int i = 0; i < I; ++i)
+            q[(size_t)m * I + i] = (int8_t)rintf((r[i] * 127.0f) * inv);
+        scale[m] = amax * (1.0f / 127.0f);
+    }
+}
+
+ORC_API void orc_gmm2_int8(const int8_t *Hq, const float *Hs, const int64_t *cnt, int L, const int8_t *W2,
+                           const float *W2s, int I, int H, uint16_t *out)
+{
+    int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
+    seg_offsets(cnt, L, off);
+    for (int e = 0; e < L; ++e) {
+        const int8_t *W = W2 + (size_t)e * H * I;
+        const float *Ws = W2s + (size_t)e * H;
+        for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            const int8_t *a = Hq + (size_t)m * I;
+            for (int n = 0; n < H; ++n) {
+                const int8_t *w = W + (size_t)n * I;
+                int32_t s = 0;
+                for (int i = 0; i < I; ++i)
+                    s += (int32_t)a[i] * (int32_t)w[i];
+                out[(size_t)m * H + n] = f32_to_bf16(((float)s * Ws[n]) * Hs[m]);
+            }
+        }
+    }
     free(off);
 }

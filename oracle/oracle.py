@@ -107,6 +107,24 @@ def dispatch(x_bf16, topk_idx, send_offset, send_token_idx, E, quant_mode, n_row
     return ex, sc, eidx
 
 
+def dispatch_int8_fused(x_bf16, topk_idx, send_offset, send_token_idx, E, smooth=None, n_rows=None):
+    """Fused-op int8 dispatch (cam_moe_distribute_dispatch.h:640-681): per destination row,
+    optional smooth[e] multiply, s = 127/amax, q = rint(f*s), scale = 1/s -> (q, scale, expand_idx)."""
+    x = _c(x_bf16, np.uint16)
+    T, H = x.shape
+    ti = _c(topk_idx, np.int32)
+    K = ti.shape[1]
+    if n_rows is None:
+        n_rows = int(((ti >= 0) & (ti < E)).sum())
+    ex = np.zeros((n_rows, H), np.int8)
+    sc = np.zeros(n_rows, np.float32)
+    eidx = np.full((n_rows, 3), -7, np.int32)
+    sm = None if smooth is None else _c(smooth, np.float32)
+    lib().orc_dispatch_int8_fused(_p(x), _p(ti), _p(_c(send_offset, np.int32)), _p(_c(send_token_idx, np.int32)),
+                                  T, H, K, E, _p(sm), _p(ex), _p(sc), _p(eidx))
+    return ex, sc, eidx
+
+
 def combine(y_bf16, expand_idx, topk_idx, topk_w, E):
     """C1 (moe_combine_normal.h:343-377; cam_moe_distribute_combine.h:654-716)."""
     y = _c(y_bf16, np.uint16)
@@ -194,3 +212,35 @@ def f32_to_bf16(f):
 def e4m3_table():
     """All 256 e4m3fn codes decoded to float32 (NaN at 0x7f/0xff)."""
     return np.array([lib().orc_e4m3_to_f32(c) for c in range(256)], np.float32)
+
+
+def gmm1_swiglu_int8(A, As, counts, W1, W1s):
+    """int8 GMM1 + SwiGLU with per-channel / per-token dequant -> h fp32 [M, I]."""
+    A = _c(A, np.int8)
+    W1 = _c(W1, np.int8)
+    L, I2, H = W1.shape
+    h = np.zeros((A.shape[0], I2 // 2), np.float32)
+    lib().orc_gmm1_swiglu_int8(_p(A), _p(_c(As, np.float32)), _p(_c(counts, np.int64)), L, _p(W1),
+                               _p(_c(W1s, np.float32)), H, I2 // 2, _p(h))
+    return h
+
+
+def quant_rows_int8(h):
+    """Per-token int8 requant of h (post_swiglu_dynamic_quant.h:164-231) -> (q int8, scale)."""
+    h = _c(h, np.float32)
+    M, I = h.shape
+    q = np.zeros((M, I), np.int8)
+    s = np.zeros(M, np.float32)
+    lib().orc_quant_rows_int8(_p(h), M, I, _p(q), _p(s))
+    return q, s
+
+
+def gmm2_int8(Hq, Hs, counts, W2, W2s):
+    """int8 GMM2 with per-channel / per-token dequant -> bf16 [M, H]."""
+    Hq = _c(Hq, np.int8)
+    W2 = _c(W2, np.int8)
+    L, H, I = W2.shape
+    out = np.zeros((Hq.shape[0], H), np.uint16)
+    lib().orc_gmm2_int8(_p(Hq), _p(_c(Hs, np.float32)), _p(_c(counts, np.int64)), L, _p(W2),
+                        _p(_c(W2s, np.float32)), I, H, _p(out))
+    return out

@@ -197,7 +197,11 @@ def test_fused_rejects_unsupported(ops):
     with pytest.raises(RuntimeError, match="one EP rank"):
         ops.fused_deep_moe(d["x"], d["ids"], [d["w1"].transpose(1, 2)], [], [d["w2"].transpose(1, 2)], [],
                            d["scales"], None, None, None, None, None, None, None, "ep", 2, 0, 8, 0, 0)
-    with pytest.raises(RuntimeError, match="int8"):
-        w = torch.zeros(8, 1024, 256, dtype=torch.int8, device="cuda")
+    with pytest.raises(RuntimeError, match="not supported"):
+        w = torch.zeros(8, 1024, 256, dtype=torch.float16, device="cuda")
         ops.fused_deep_moe(d["x"], d["ids"], [w], [], [w], [], d["scales"], None, None, None, None, None, None,
                            None, "ep", 1, 0, 8, 0, 0)
+    with pytest.raises(RuntimeError, match="need int8 weights"):
+        sm = torch.ones(8, 1024, device="cuda")
+        ops.fused_deep_moe(d["x"], d["ids"], [d["w1"].transpose(1, 2)], [], [d["w2"].transpose(1, 2)], [],
+                           d["scales"], None, None, None, None, sm, None, None, "ep", 1, 0, 8, 0, 0)

@@ -1,0 +1,252 @@
+"""GPU parity of the int8 W8A8 path -- the reference's own fused numerics:
+per-token dynamic int8 activations, int8 weights with per-channel scales,
+exact int32 accumulation, per-channel x per-token dequantisation, SwiGLU,
+per-token requantisation of h (fused_deep_moe's GMM1/GMM2 epilogues and
+post_swiglu_dynamic_quant.h:164-231).
+
+Bars:
+  * GMM2 from the same int8 input: bit-exact with the oracle (integer sums are
+    exact and the epilogue is a fixed fp32 sequence).
+  * GMM1+SwiGLU+requant: the fp32 h differs from the oracle's only by the last
+    ulps of exp(), so the per-token scale matches to 1e-5 relative and an int8
+    code may move by one where h sits on a rounding boundary (at most 1 in 1000).
+  * fused_deep_moe int8 vs the oracle chain: expert_token_nums exact, output
+    within 2e-2 relative (max-norm) -- the requantisation's rare one-code flips
+    are the only difference.
+Test data follow the reference test's recipe (test_fused_deep_moe.py:276-344):
+x ~ U(-5, 5), weights randint(-16, 16), per-channel scales U(0.0015, 0.0045).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import umdk_amd  # noqa: F401
+    return torch.ops.umdk_cam_op_lib
+
+
+def relerr(got, ref):
+    got = torch.as_tensor(got, dtype=torch.float64)
+    ref = torch.as_tensor(ref, dtype=torch.float64)
+    return ((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def b16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def w_int8(g, shape):
+    return torch.randint(-16, 16, shape, generator=g).to(torch.int8)
+
+
+def ch_scale(g, shape):
+    return torch.rand(shape, generator=g) * 0.003 + 0.0015
+
+
+def check_requant(hq, hs, q_ref, s_ref):
+    hq = hq.cpu().numpy().astype(np.int32)
+    hs = hs.cpu().numpy()
+    np.testing.assert_allclose(hs, s_ref, rtol=1e-5, atol=0)
+    d = np.abs(hq - q_ref.astype(np.int32))
+    assert d.max() <= 1, f"int8 code off by {d.max()}"
+    assert (d > 0).mean() <= 1e-3, f"{(d > 0).mean():.2e} of the codes moved"
+
+
+# rows per expert, H (k of GMM1), I; the first two take the 32-row tile, the others the 8-wave kernel
+CASES = [([3, 40, 0, 7], 1024, 256), ([1], 512, 128), ([5, 0, 300], 256, 256), ([17, 256, 255, 1, 0, 9], 512, 128)]
+
+
+@pytest.mark.parametrize("counts,H,I", CASES)
+def test_int8_gmm1_swiglu_requant_vs_oracle(ops, counts, H, I):
+    print(f"int8 gmm1 counts={counts} H={H} I={I}", flush=True)
+    g = gen(sum(counts) + H)
+    L, M = len(counts), sum(counts)
+    x = torch.randint(-127, 128, (M, H), generator=g).to(torch.int8)
+    xs = torch.rand(M, generator=g) * 0.04
+    w1 = w_int8(g, (L, 2 * I, H))
+    s1 = ch_scale(g, (L, 2 * I))
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    hq, hs = ops.grouped_matmul_swiglu(x.cuda(), xs.cuda(), cnt.cuda(), w1.cuda(), s1.cuda(), 2)
+    h_ref = orc.gmm1_swiglu_int8(x.numpy(), xs.numpy(), cnt.numpy(), w1.numpy(), s1.numpy())
+    q_ref, s_ref = orc.quant_rows_int8(h_ref)
+    check_requant(hq, hs, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("counts,H,I", CASES)
+def test_int8_gmm2_bit_exact_vs_oracle(ops, counts, H, I):
+    print(f"int8 gmm2 counts={counts} H={H} I={I}", flush=True)
+    g = gen(7 + sum(counts))
+    L, M = len(counts), sum(counts)
+    hq = torch.randint(-127, 128, (M, I), generator=g).to(torch.int8)
+    hs = torch.rand(M, generator=g) * 0.01
+    w2 = w_int8(g, (L, H, I))
+    s2 = ch_scale(g, (L, H))
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    y = ops.grouped_matmul(hq.cuda(), hs.cuda(), cnt.cuda(), w2.cuda(), s2.cuda())
+    ref = orc.gmm2_int8(hq.numpy(), hs.numpy(), cnt.numpy(), w2.numpy(), s2.numpy())
+    assert np.array_equal(b16(y), ref)
+
+
+def test_int8_gemm_large_vs_torch(ops):
+    # prefill-sized rows per expert (the 8-wave kernel, 256-row tile): exact int64 sums on the CPU
+    counts, H, I = [700, 0, 1100, 520], 1024, 256
+    print(f"int8 large counts={counts}", flush=True)
+    g = gen(99)
+    L, M = len(counts), sum(counts)
+    cap = M + 64                                   # capacity beyond the routed rows
+    x = torch.randint(-127, 128, (cap, H), generator=g).to(torch.int8)
+    xs = torch.rand(cap, generator=g) * 0.04
+    w2 = w_int8(g, (L, H, 2 * I))
+    s2 = ch_scale(g, (L, H))
+    hin = torch.randint(-127, 128, (cap, 2 * I), generator=g).to(torch.int8)
+    hs = torch.rand(cap, generator=g) * 0.01
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    y = ops.grouped_matmul(hin.cuda(), hs.cuda(), cnt.cuda(), w2.cuda(), s2.cuda()).cpu()
+    off = [0] + list(np.cumsum(counts))
+    for e in range(L):
+        r = slice(off[e], off[e + 1])
+        acc = hin[r].long() @ w2[e].T.long()
+        ref = ((acc.float() * s2[e]) * hs[r, None]).bfloat16()
+        assert torch.equal(y[r].view(torch.int16), ref.view(torch.int16))
+    w1 = w_int8(g, (L, 2 * I, H))
+    s1 = ch_scale(g, (L, 2 * I))
+    hq, hsc = ops.grouped_matmul_swiglu(x.cuda(), xs.cuda(), cnt.cuda(), w1.cuda(), s1.cuda(), 2)
+    h_ref = orc.gmm1_swiglu_int8(x[:M].numpy(), xs[:M].numpy(), cnt.numpy(), w1.numpy(), s1.numpy())
+    q_ref, s_ref = orc.quant_rows_int8(h_ref)
+    check_requant(hq[:M], hsc[:M], q_ref, s_ref)
+
+
+def make_fused(seed, bs, H, I, E, K, ish=0, smooth=False):
+    g = gen(seed)
+    d = dict(x=(torch.rand(bs, H, generator=g) * 10 - 5).bfloat16(),
+             ids=torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(bs)]).int(),
+             scales=torch.rand(bs, K, generator=g),
+             w1=w_int8(g, (E, H, 2 * I)), s1=ch_scale(g, (E, 2 * I)),       # reference logical layouts
+             w2=w_int8(g, (E, I, H)), s2=ch_scale(g, (E, H)))
+    if ish:
+        sw1 = torch.full((H, 2 * ish), 4, dtype=torch.int8)                 # test_fused_deep_moe.py:321-326
+        sw2 = torch.full((ish, H), 4, dtype=torch.int8)
+        sw1[:, ::2] *= -1
+        sw2[:, ::2] *= -1
+        d.update(sw1=sw1, sw2=sw2, ss1=torch.full((2 * ish,), 0.0015), ss2=torch.full((H,), 0.0015))
+    if smooth:
+        d.update(sm=torch.rand(E, H, generator=g) + 0.5, ssm=torch.rand(H, generator=g) + 0.5)
+    return d
+
+
+def fused_call(ops, d, E, mask=None, separated=False):
+    c = {k: (v.cuda() if torch.is_tensor(v) else v) for k, v in d.items()}
+    g1 = list(c["w1"].unbind(0)) if separated else [c["w1"]]
+    g2 = list(c["w2"].unbind(0)) if separated else [c["w2"]]
+    s1 = list(c["s1"].unbind(0)) if separated else [c["s1"]]
+    s2 = list(c["s2"].unbind(0)) if separated else [c["s2"]]
+    return ops.fused_deep_moe(c["x"], c["ids"], g1, s1, g2, s2, c["scales"], c.get("sw1"), c.get("ss1"),
+                              c.get("sw2"), c.get("ss2"), c.get("sm"), c.get("ssm"),
+                              None if mask is None else mask.cuda(), "ep", 1, 0, E, 0, 0)
+
+
+def oracle_moe(d, ids, E):
+    """Oracle chain: layout, fused int8 dispatch, GMM1+SwiGLU, requant, GMM2, combine."""
+    x = b16(d["x"])
+    _, nte, _, sti = orc.dispatch_layout(ids.astype(np.int64), E, 1)
+    so, _, _, _ = orc.notify_dispatch(nte)
+    cnt = nte.astype(np.int64)
+    sm = d["sm"].numpy() if "sm" in d else None
+    ex, xs, eidx = orc.dispatch_int8_fused(x, ids, so, sti, E, smooth=sm)
+    w1 = d["w1"].transpose(1, 2).contiguous().numpy()
+    w2 = d["w2"].transpose(1, 2).contiguous().numpy()
+    h = orc.gmm1_swiglu_int8(ex, xs, cnt, w1, d["s1"].numpy())
+    hq, hs = orc.quant_rows_int8(h)
+    y = orc.gmm2_int8(hq, hs, cnt, w2, d["s2"].numpy())
+    return orc.combine(y, eidx, ids, d["scales"].numpy(), E), nte
+
+
+def oracle_shared(d):
+    T = d["x"].shape[0]
+    ids0 = np.zeros((T, 1), np.int32)
+    ssm = d["ssm"].numpy()[None] if "ssm" in d else None
+    ex, xs, _ = orc.dispatch_int8_fused(b16(d["x"]), ids0, np.zeros(1, np.int32), np.arange(T, dtype=np.int32), 1,
+                                        smooth=ssm)
+    cnt = np.array([T], np.int64)
+    h = orc.gmm1_swiglu_int8(ex, xs, cnt, d["sw1"].T.contiguous().numpy()[None], d["ss1"].numpy()[None])
+    hq, hs = orc.quant_rows_int8(h)
+    return orc.gmm2_int8(hq, hs, cnt, d["sw2"].T.contiguous().numpy()[None], d["ss2"].numpy()[None])
+
+
+@pytest.mark.parametrize("bs,H,I,E,K,smooth", [(16, 1024, 256, 16, 8, False), (24, 2048, 128, 8, 4, True),
+                                               (3, 1024, 128, 8, 2, False)])
+def test_fused_int8_vs_oracle_chain(ops, bs, H, I, E, K, smooth):
+    print(f"fused int8 bs={bs} H={H} I={I} E={E} K={K} smooth={smooth}", flush=True)
+    d = make_fused(bs * 31 + H, bs, H, I, E, K, smooth=smooth)
+    out, _, etn = fused_call(ops, d, E)
+    ref, nte = oracle_moe(d, d["ids"].numpy(), E)
+    assert np.array_equal(etn.cpu().numpy(), nte.astype(np.int64))
+    assert relerr(out.cpu().float(), orc.bf16_to_f32(ref)) < 2e-2
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_fused_int8_shared_mask_separated(ops, smooth):
+    bs, H, I, E, K, ish = 12, 1024, 128, 8, 3, 256
+    print(f"fused int8 shared smooth={smooth}", flush=True)
+    d = make_fused(17, bs, H, I, E, K, ish=ish, smooth=smooth)
+    d["ids"][2, 1] = -1
+    mask = torch.ones(bs, dtype=torch.bool)
+    mask[9:] = False
+    out, sh, etn = fused_call(ops, d, E, mask=mask)
+    out_s, sh_s, etn_s = fused_call(ops, d, E, mask=mask, separated=True)
+    assert torch.equal(out.view(torch.int16), out_s.view(torch.int16)) and torch.equal(etn, etn_s)
+    assert torch.equal(sh.view(torch.int16), sh_s.view(torch.int16))
+    rid = d["ids"].numpy().copy()
+    rid[9:] = -1
+    ref, nte = oracle_moe(d, rid, E)
+    assert np.array_equal(etn.cpu().numpy(), nte.astype(np.int64))
+    got = out.cpu().float()
+    assert relerr(got[:9], orc.bf16_to_f32(ref)[:9]) < 2e-2
+    assert (got[9:] == 0).all()
+    assert relerr(sh.cpu().float(), orc.bf16_to_f32(oracle_shared(d))) < 2e-2
+
+
+def test_fused_int8_graph_replays(ops):
+    bs, H, I, E, K = 64, 2048, 256, 16, 8
+    d = make_fused(3, bs, H, I, E, K)
+    eager, _, etn0 = fused_call(ops, d, E)
+    c = {k: (v.cuda() if torch.is_tensor(v) else v) for k, v in d.items()}
+    args = (c["x"], c["ids"], [c["w1"]], [c["s1"]], [c["w2"]], [c["s2"]], c["scales"], None, None, None, None, None,
+            None, None, "ep", 1, 0, E, 0, 0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            ops.fused_deep_moe(*args)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, _, getn = ops.fused_deep_moe(*args)
+    for r in range(3):
+        junk = torch.randn(1 << 20, device="cuda") * r
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout.view(torch.int16), eager.view(torch.int16)), f"replay {r}"
+        assert torch.equal(getn, etn0)
+        del junk
+
+
+def test_int8_rejects_bad_scales(ops):
+    x = torch.zeros(4, 256, dtype=torch.int8, device="cuda")
+    w = torch.zeros(1, 256, 256, dtype=torch.int8, device="cuda")
+    cnt = torch.tensor([4], dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="per channel"):
+        ops.grouped_matmul(x, torch.ones(4, device="cuda"), cnt, w, torch.ones(1, 2, 2, device="cuda"))
+    with pytest.raises(RuntimeError, match="out_quant=2"):
+        ops.grouped_matmul_swiglu(x, torch.ones(4, device="cuda"), cnt, w, torch.ones(1, 256, device="cuda"), 0)

@@ -329,11 +329,11 @@ static camhipStatus check_gmm(const char *op, const void *x, const float *xScale
                               int64_t numGroups, int64_t m, int64_t k, int64_t n, const void *weight,
                               const float *weightScale, int64_t dtype, bool swiglu)
 {
-    CHECK_PARAM(dtype == CAMHIP_DTYPE_BF16 || dtype == CAMHIP_DTYPE_FP8, "%s: dtype %lld not supported (0 or 3)", op,
-                (long long)dtype);
+    CHECK_PARAM(dtype == CAMHIP_DTYPE_BF16 || dtype == CAMHIP_DTYPE_INT8 || dtype == CAMHIP_DTYPE_FP8,
+                "%s: dtype %lld not supported (0, 2 or 3)", op, (long long)dtype);
     CHECK_PARAM(numGroups >= 1 && numGroups <= 512, "%s: numGroups %lld out of [1,512]", op, (long long)numGroups);
     CHECK_PARAM(m >= 1 && m <= (1 << 24), "%s: m %lld out of range", op, (long long)m);
-    const int64_t esz = dtype == CAMHIP_DTYPE_FP8 ? 1 : 2;
+    const int64_t esz = dtype == CAMHIP_DTYPE_BF16 ? 2 : 1;
     CHECK_PARAM(k >= 128 / esz && (k * esz) % 128 == 0, "%s: k %lld must be a multiple of %lld", op, (long long)k,
                 (long long)(128 / esz));
     if (swiglu)
@@ -346,7 +346,7 @@ static camhipStatus check_gmm(const char *op, const void *x, const float *xScale
     CHECK_PTR(x);
     CHECK_PTR(groupList);
     CHECK_PTR(weight);
-    if (dtype == CAMHIP_DTYPE_FP8) {
+    if (dtype != CAMHIP_DTYPE_BF16) {
         CHECK_PTR(xScale);
         CHECK_PTR(weightScale);
     }
@@ -363,9 +363,33 @@ camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(const void *x, const floa
                                 weightScale, dtype, true);
     if (st != CAMHIP_SUCCESS)
         return st;
+    CHECK_PTR(h);
+    if (dtype == CAMHIP_DTYPE_INT8) {
+        // int32 GEMM, fp32 h and its row amax in the workspace, then the per-token int8 requantisation
+        CHECK_PARAM(outQuant == CAMHIP_QUANT_INT8_TOKEN, "grouped_matmul_swiglu: int8 inputs need outQuant 2 (got %lld)",
+                    (long long)outQuant);
+        CHECK_PTR(hScale);
+        const uint64_t h_off = 0, amax_off = ((uint64_t)m * (n / 2) * 4 + 255) & ~(uint64_t)255;
+        const uint64_t ws_bytes = amax_off + (uint64_t)m * 4;
+        const int L = (int)numGroups, M = (int)m, I = (int)(n / 2);
+        const cam::GmmArgs base{(const uint8_t *)x, xScale, groupList, L, M, (int)k, (int)n,
+                                (const uint8_t *)weight, weightScale, nullptr, nullptr};
+        return make_executor(
+            ws_bytes,
+            [=](void *ws, hipStream_t s) {
+                cam::GmmArgs a = base;
+                float *hf = (float *)((uint8_t *)ws + h_off), *amax = (float *)((uint8_t *)ws + amax_off);
+                a.C = (uint8_t *)hf;
+                a.Cs = amax;
+                hipError_t e = cam::launch_gmm(a, cam::DT_INT8, cam::EPI_SWIGLU_F32AMAX, s);
+                if (e != hipSuccess)
+                    return e;
+                return cam::launch_quant_rows_int8(hf, amax, groupList, L, M, I, (int8_t *)h, hScale, s);
+            },
+            workspaceSize, executor);
+    }
     CHECK_PARAM(outQuant == CAMHIP_QUANT_NONE || outQuant == CAMHIP_QUANT_FP8_BLOCK,
                 "grouped_matmul_swiglu: outQuant %lld not supported (0 or 3)", (long long)outQuant);
-    CHECK_PTR(h);
     if (outQuant == CAMHIP_QUANT_FP8_BLOCK)
         CHECK_PTR(hScale);
     cam::GmmArgs a{(const uint8_t *)x, xScale, groupList, (int)numGroups, (int)m, (int)k, (int)n,

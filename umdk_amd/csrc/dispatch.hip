@@ -11,6 +11,8 @@
 //   quant_mode 0: bf16 copy.
 //   quant_mode 2: int8 per token, s = 127/(amax+1e-12), q = rint(x*s), scale = 1/s
 //                 (moe_dispatch_normal.h:295-332).
+//   QUANT_INT8_FUSED (internal, the fused decode op): int8 per token, optional
+//                 per-expert smooth scales, s = 127/amax (dispatch_int8_kernel).
 //   quant_mode 3: fp8 e4m3fn per 1x128 block: amax clamped to >= 1e-4,
 //                 q = e4m3_rne_sat(x * (448/amax)), scale = amax/448.  A block
 //                 is 8 adjacent lanes, so its amax is a 3-step xor shuffle.
@@ -133,11 +135,18 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
 
 // int8 per-token quantisation needs the whole row's amax: one wave per token,
 // the row held in registers (lane l owns columns [1024 j + 16 l, +16)).
+// FUSED = false: the prefill recipe, s = 127/(amax+1e-12) (moe_dispatch_normal.h:295-332).
+// FUSED = true: the fused decode recipe (cam_moe_distribute_dispatch.h:640-681 and the shared-expert
+// QuantToken, grouped_matmul_slice_m_per_token_dequant_swiglu_quant_multistage_workspace.h): optional
+// smooth scales smooth[e, :] multiply x first (e = the destination expert, 0 in identity mode), then
+// s = 127/amax with no epsilon; a row of zeros gets q = 0 and scale 0.  With smooth scales the
+// quantised row differs per destination, so it is recomputed for each of the token's K rows.
+template <bool FUSED>
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
     const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap,
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
-    int32_t *__restrict__ inv_out)
+    int32_t *__restrict__ inv_out, const float *__restrict__ smooth)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -160,40 +169,69 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
             raw[j][1] = u32x4{0, 0, 0, 0};
         }
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < DISP_NIT; ++j) {
-        float f[16];
-        unpack_bf16x8(raw[j][0], f);
-        unpack_bf16x8(raw[j][1], f + 8);
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            amax = fmaxf(amax, fabsf(f[i]));
-    }
-    amax = group_max<64>(amax);
-    const float sc = 127.0f / (amax + 1e-12f);
-    const float tok_scale = 1.0f / sc;
     u32x4 q[DISP_NIT];
+    float tok_scale = 0.0f;
+    // quantises the register row, multiplied by sm[col] when sm is given
+    auto quantise = [&](const float *sm) {
+        float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < DISP_NIT; ++j) {
-        float f[16];
-        unpack_bf16x8(raw[j][0], f);
-        unpack_bf16x8(raw[j][1], f + 8);
+        for (int j = 0; j < DISP_NIT; ++j) {
+            float f[16];
+            unpack_bf16x8(raw[j][0], f);
+            unpack_bf16x8(raw[j][1], f + 8);
+            const int col = j * 1024 + lane * 16;
+            if (sm && col < H) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            uint32_t pk = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int v = (int)rintf(f[4 * w + b] * sc);
-                pk |= (uint32_t)(v & 0xff) << (8 * b);
+                for (int i = 0; i < 16; ++i)
+                    f[i] = f[i] * sm[col + i];
             }
-            q[j][w] = pk;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                amax = fmaxf(amax, fabsf(f[i]));
         }
-    }
+        amax = group_max<64>(amax);
+        float sc;
+        if (FUSED) {
+            sc = amax > 0.0f ? 127.0f / amax : 0.0f;
+            tok_scale = amax > 0.0f ? 1.0f / sc : 0.0f;
+        } else {
+            sc = 127.0f / (amax + 1e-12f);
+            tok_scale = 1.0f / sc;
+        }
+#pragma unroll
+        for (int j = 0; j < DISP_NIT; ++j) {
+            float f[16];
+            unpack_bf16x8(raw[j][0], f);
+            unpack_bf16x8(raw[j][1], f + 8);
+            const int col = j * 1024 + lane * 16;
+            if (sm && col < H) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    f[i] = f[i] * sm[col + i];
+            }
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int v = (int)rintf(f[4 * w + b] * sc);
+                    pk |= (uint32_t)(v & 0xff) << (8 * b);
+                }
+                q[j][w] = pk;
+            }
+        }
+    };
+    const bool per_dest = FUSED && smooth != nullptr;
+    if (!per_dest)
+        quantise(nullptr);
     for (int k = 0; k < K; ++k) {
         const int row = __shfl(dst, k, 64);
         if (row < 0)
             continue;
+        if (per_dest) {
+            const int e = topk_idx ? topk_idx[(size_t)t * K + k] : 0;
+            quantise(smooth + (size_t)e * H);
+        }
         u32x4 *out = reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H);
 #pragma unroll
         for (int j = 0; j < DISP_NIT; ++j) {
@@ -214,7 +252,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
-                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out)
+                           void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out,
+                           const float *smooth)
 {
     if (T == 0)
         return hipSuccess;
@@ -230,8 +269,14 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
                            send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out);
         break;
     case QUANT_INT8_TOKEN:
-        hipLaunchKernelGGL(dispatch_int8_kernel, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x, topk_idx,
-                           send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx, inv_out);
+        hipLaunchKernelGGL(dispatch_int8_kernel<false>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
+                           topk_idx, send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx,
+                           inv_out, nullptr);
+        break;
+    case QUANT_INT8_FUSED:
+        hipLaunchKernelGGL(dispatch_int8_kernel<true>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
+                           topk_idx, send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx,
+                           inv_out, smooth);
         break;
     case QUANT_FP8_BLOCK:
         if (H & 127)

@@ -43,17 +43,24 @@ struct Carve {
 };
 
 struct FusedLayout {
-    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv;
-    uint64_t sh_x, sh_xs, sh_h, sh_hs, sh_gl;
+    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv, hf, amax;
+    uint64_t sh_x, sh_xs, sh_h, sh_hs, sh_gl, sh_hf, sh_amax;
     uint64_t bytes;
 };
 
-FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, bool fp8, bool shared)
+// Scale bytes per row of `cols` elements: fp8 one float per 128, int8 one per row, bf16 none.
+static uint64_t scale_bytes(int dt, uint64_t cols)
+{
+    return dt == cam::DT_FP8 ? cols / 128 * 4 : dt == cam::DT_INT8 ? 4 : 0;
+}
+
+FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool shared)
 {
     Carve c;
     FusedLayout f{};
     const uint64_t N = (uint64_t)T * K;
-    const uint64_t esz = fp8 ? 1 : 2;
+    const uint64_t esz = dt == cam::DT_BF16 ? 2 : 1;
+    const bool int8 = dt == cam::DT_INT8;
     f.ids = c.take(4 * N);
     f.layout_ws = c.take(cam::layout_workspace_bytes(T, K, L, 1));
     f.counts = c.take(4 * (uint64_t)L);
@@ -62,18 +69,22 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, bool fp8, boo
     f.total = c.take(4);
     f.sti = c.take(4 * N);
     f.ex = c.take(N * H * esz);
-    f.xs = c.take(fp8 ? N * (H / 128) * 4 : 0);
+    f.xs = c.take(N * scale_bytes(dt, H));
     f.eidx = c.take(12 * N);
     f.h = c.take(N * I * esz);
-    f.hs = c.take(fp8 ? N * (I / 128) * 4 : 0);
+    f.hs = c.take(N * scale_bytes(dt, I));
     f.y = c.take(N * H * 2);
     f.inv = c.take(4 * N);
+    f.hf = c.take(int8 ? N * I * 4 : 0);  // int8: fp32 h and its row maxima before the requantisation
+    f.amax = c.take(int8 ? N * 4 : 0);
     if (shared) {
         f.sh_x = c.take((uint64_t)T * H * esz);
-        f.sh_xs = c.take(fp8 ? (uint64_t)T * (H / 128) * 4 : 0);
+        f.sh_xs = c.take((uint64_t)T * scale_bytes(dt, H));
         f.sh_h = c.take((uint64_t)T * Ish * esz);
-        f.sh_hs = c.take(fp8 ? (uint64_t)T * (Ish / 128) * 4 : 0);
+        f.sh_hs = c.take((uint64_t)T * scale_bytes(dt, Ish));
         f.sh_gl = c.take(8);
+        f.sh_hf = c.take(int8 ? (uint64_t)T * Ish * 4 : 0);
+        f.sh_amax = c.take(int8 ? (uint64_t)T * 4 : 0);
     }
     f.bytes = c.off;
     return f;
@@ -125,23 +136,25 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
     F_CHECK(weightDtype != CAMHIP_DTYPE_FP8 || (gmm1HiddenSize / 2 <= 16384 && shareGmm1HiddenSize / 2 <= 16384),
             "fused_deep_moe: fp8 intermediate sizes above 16384 are not supported");
-    F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_FP8,
-            "fused_deep_moe: weight dtype %lld not supported (bf16 or fp8 e4m3fn)", (long long)weightDtype);
+    F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_INT8 || weightDtype == CAMHIP_DTYPE_FP8,
+            "fused_deep_moe: weight dtype %lld not supported (bf16, int8 or fp8 e4m3fn)", (long long)weightDtype);
     F_CHECK(quantMode == 0, "fused_deep_moe: quant_mode is reserved and must be 0 (got %lld)", (long long)quantMode);
     F_CHECK(globalBs >= 0 && globalBs % epRankSize == 0, "fused_deep_moe: global_bs %lld invalid",
             (long long)globalBs);
-    F_CHECK(expertSmoothScales == nullptr && shareSmoothScales == nullptr,
-            "fused_deep_moe: smooth-quant scales are not supported by this build");
+    F_CHECK(weightDtype == CAMHIP_DTYPE_INT8 || (expertSmoothScales == nullptr && shareSmoothScales == nullptr),
+            "fused_deep_moe: smooth-quant scales need int8 weights");
     const bool shared = shareGmm1Weight != nullptr;
     F_CHECK(shared == (shareGmm2Weight != nullptr),
             "fused_deep_moe: shared-expert weights must be given together");
-    const bool fp8 = weightDtype == CAMHIP_DTYPE_FP8;
+    if (!shared)  // the reference's test passes share_smooth_scales with or without a shared expert
+        shareSmoothScales = nullptr;
+    const bool quantised = weightDtype != CAMHIP_DTYPE_BF16;
     if (shared) {
         F_CHECK(shareGmm1HiddenSize >= 256 && shareGmm1HiddenSize % 256 == 0,
                 "fused_deep_moe: share gmm1 hidden size %lld must be a multiple of 256",
                 (long long)shareGmm1HiddenSize);
         F_PTR(shareOutput);
-        if (fp8) {
+        if (quantised) {
             F_PTR(shareGmm1WeightScale);
             F_PTR(shareGmm2WeightScale);
         }
@@ -149,7 +162,7 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
     F_PTR(gmm1Weight);
     F_PTR(gmm2Weight);
     F_PTR(expertTokenNums);
-    if (fp8) {
+    if (quantised) {
         F_PTR(gmm1WeightScale);
         F_PTR(gmm2WeightScale);
     }
@@ -163,11 +176,23 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
 
     const int T = (int)batchSize, H = (int)hidden, K = (int)topK, L = (int)(moeExpertNum / epRankSize);
     const int I = (int)(gmm1HiddenSize / 2), Ish = (int)(shareGmm1HiddenSize / 2);
-    const FusedLayout f = plan_fused(T, H, K, L, I, shared ? Ish : 0, fp8, shared);
+    const int dt = (int)weightDtype;  // CAMHIP_DTYPE_* equal cam::DT_*
+    const bool int8 = dt == cam::DT_INT8;
+    const FusedLayout f = plan_fused(T, H, K, L, I, shared ? Ish : 0, dt, shared);
     const int N = T * K;
-    const int dt = fp8 ? cam::DT_FP8 : cam::DT_BF16;
-    const int q = fp8 ? cam::QUANT_FP8_BLOCK : cam::QUANT_NONE;
-    const int epi1 = fp8 ? cam::EPI_SWIGLU_FP8 : cam::EPI_SWIGLU_BF16;
+    const int q = dt == cam::DT_FP8 ? cam::QUANT_FP8_BLOCK : int8 ? cam::QUANT_INT8_FUSED : cam::QUANT_NONE;
+    const int epi1 = dt == cam::DT_FP8 ? cam::EPI_SWIGLU_FP8 : int8 ? cam::EPI_SWIGLU_F32AMAX : cam::EPI_SWIGLU_BF16;
+    // GMM1 + SwiGLU: int8 writes fp32 h and row maxima, then requantises per token
+    auto gmm1 = [=](cam::GmmArgs a, float *hf, float *amax, hipStream_t s) -> hipError_t {
+        if (!int8)
+            return cam::launch_gmm(a, dt, epi1, s);
+        int8_t *hq = (int8_t *)a.C;
+        float *hs = a.Cs;
+        a.C = (uint8_t *)hf;
+        a.Cs = amax;
+        HIP_TRY(cam::launch_gmm(a, dt, epi1, s));
+        return cam::launch_quant_rows_int8(hf, amax, a.group_list, a.L, a.M, a.N / 2, hq, hs, s);
+    };
 
     auto fn = [=](void *wsv, hipStream_t s) -> hipError_t {
         uint8_t *ws = (uint8_t *)wsv;
@@ -190,10 +215,11 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         }
         // dispatch also writes the combine's row map (inv), so the combine is a single gather
         HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
-                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv)));
+                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv),
+                                     expertSmoothScales));
         cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
                         (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
-        HIP_TRY(cam::launch_gmm(g1, dt, epi1, s));
+        HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), s));
         cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
                         (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
         HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
@@ -206,15 +232,15 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             HIP_TRY(cam::launch_fill_i64(gl, T, 1, s));
             const void *sx = x;
             const float *sxs = nullptr;
-            if (fp8) {
+            if (dt != cam::DT_BF16) {
                 HIP_TRY(cam::launch_dispatch(x, nullptr, nullptr, nullptr, T, H, 1, 1, 0, T, q, P(f.sh_x),
-                                             (float *)P(f.sh_xs), nullptr, s));
+                                             (float *)P(f.sh_xs), nullptr, s, nullptr, shareSmoothScales));
                 sx = P(f.sh_x);
                 sxs = (const float *)P(f.sh_xs);
             }
             cam::GmmArgs s1{(const uint8_t *)sx, sxs, gl, 1, T, H, 2 * Ish, (const uint8_t *)shareGmm1Weight,
                             shareGmm1WeightScale, (uint8_t *)P(f.sh_h), (float *)P(f.sh_hs)};
-            HIP_TRY(cam::launch_gmm(s1, dt, epi1, s));
+            HIP_TRY(gmm1(s1, (float *)P(f.sh_hf), (float *)P(f.sh_amax), s));
             cam::GmmArgs s2{(const uint8_t *)P(f.sh_h), (const float *)P(f.sh_hs), gl, 1, T, Ish, H,
                             (const uint8_t *)shareGmm2Weight, shareGmm2WeightScale, (uint8_t *)shareOutput,
                             nullptr};

@@ -5,25 +5,32 @@
 
 namespace cam {
 
-enum GmmDtype { DT_BF16 = 0, DT_FP8 = 3 };
-enum GmmEpilogue { EPI_PLAIN = 0, EPI_SWIGLU_BF16 = 1, EPI_SWIGLU_FP8 = 2 };
+enum GmmDtype { DT_BF16 = 0, DT_INT8 = 2, DT_FP8 = 3 };
+// EPI_SWIGLU_F32AMAX (int8 only): h in fp32 [M, N/2] and, per row, max |h| over the whole row in Cs[m]
+// (float bits, combined across tiles by atomic max; the launcher clears it first), for the per-token
+// int8 requantisation that follows (launch_quant_rows_int8).
+enum GmmEpilogue { EPI_PLAIN = 0, EPI_SWIGLU_BF16 = 1, EPI_SWIGLU_FP8 = 2, EPI_SWIGLU_F32AMAX = 3 };
 
 struct GmmArgs {
     const uint8_t *A;           // [M, K] activations in dispatch order (bf16 or fp8 bytes)
-    const float *As;            // fp8: [M, K/128] activation block scales
+    const float *As;            // fp8: [M, K/128] activation block scales; int8: [M] per-token scales
     const int64_t *group_list;  // [L] rows per local expert (device)
     int L;                      // local experts
     int M;                      // rows allocated in A and the output
     int K;                      // reduction length (elements)
     int N;                      // W rows per expert (2I for SwiGLU, H for the plain GEMM)
     const uint8_t *W;           // [L, N, K]
-    const float *Ws;            // fp8: [L, N/128, K/128]
-    uint8_t *C;                 // plain: bf16 [M, N]; SwiGLU: h [M, N/2] (bf16 or fp8)
-    float *Cs;                  // SwiGLU fp8: [M, N/256] h block scales
+    const float *Ws;            // fp8: [L, N/128, K/128]; int8: [L, N] per-channel scales
+    uint8_t *C;                 // plain: bf16 [M, N]; SwiGLU: h [M, N/2] (bf16, fp8 or fp32)
+    float *Cs;                  // SwiGLU fp8: [M, N/256] h block scales; SwiGLU fp32: [M] row max |h|
     int allow256 = 1;           // set by the launcher: the 256-row tile may be picked on the device
 };
 
 size_t gmm_lds_bytes();
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);
+// Per-token int8 requantisation of the fp32 h written by EPI_SWIGLU_F32AMAX, rows [0, sum(group_list)):
+// q = rint((h * 127) * (1 / amax)), scale = amax * (1/127); rows with amax 0 get q = 0, scale 0.
+hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64_t *group_list, int L, int M, int I,
+                                  int8_t *q, float *scale, hipStream_t s);
 
 }  // namespace cam

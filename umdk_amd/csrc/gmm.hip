@@ -41,6 +41,7 @@
 //     that XCD's L2.
 #include "cam_device.h"
 #include "gmm.h"
+#include "launchers.h"
 
 namespace cam {
 
@@ -174,8 +175,9 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
     constexpr bool FP8 = DT == DT_FP8;
+    constexpr bool INT8 = DT == DT_INT8;
     constexpr int LOADS = A_LOADS + B_LOADS + (FP8 ? TC::S_DMAS : 0);  // DMA instructions per wave per stage
-    const int esz = FP8 ? 1 : 2;
+    const int esz = DT == DT_BF16 ? 2 : 1;
     const uint32_t kbytes = (uint32_t)p.K * esz;  // bytes per row
     const int nk = (int)(kbytes / GKB);
     const int half_n = p.N / 2;                    // I for SwiGLU
@@ -296,7 +298,25 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             const uint8_t *st = smem + cur * STAGE_BYTES;
             const uint8_t *la = st + (wm * WM) * GKB;
             const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
-            if constexpr (DT == DT_BF16) {
+            if constexpr (INT8) {
+                // two v_mfma_i32_16x16x64_i8 per k-step; fragments sit where the bf16 ones do
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) {
+                    i32x4 afr[IF];
+#pragma unroll
+                    for (int i = 0; i < IF; ++i)
+                        afr[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, sub * 4 + lg));
+#pragma unroll
+                    for (int j = 0; j < JF; ++j) {
+                        const i32x4 bfr = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
+#pragma unroll
+                        for (int i = 0; i < IF; ++i)
+                            acc[i][j] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                           bfr, afr[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
+                    }
+                }
+            } else if constexpr (DT == DT_BF16) {
 #pragma unroll
                 for (int sub = 0; sub < 2; ++sub) {
                     bf16x8 afr[IF];
@@ -348,6 +368,31 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
         bar();
 
+        if constexpr (INT8) {
+            // per-channel x per-token dequantisation of the exact int32 sums:
+            // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
+            const float *wsr = p.Ws + (size_t)e * p.N;
+#pragma unroll
+            for (int j = 0; j < JF; ++j) {
+                int c0;
+                if (SWIGLU) {
+                    const int jj = j % (JF / 2);
+                    c0 = n0 + (WN / 2) * wn + 16 * jj + 4 * lg + (j >= JF / 2 ? half_n : 0);
+                } else {
+                    c0 = n0 + wn * WN + 16 * j + 4 * lg;
+                }
+                const f32x4 wv = *reinterpret_cast<const f32x4 *>(wsr + c0);
+#pragma unroll
+                for (int i = 0; i < IF; ++i) {
+                    const float xs = p.As[min(row0 + wm * WM + i * 16 + l16, p.M - 1)];
+                    const i32x4 iv = __builtin_bit_cast(i32x4, acc[i][j]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[i][j][q] = ((float)iv[q] * wv[q]) * xs;
+                }
+            }
+        }
+
         // ---- epilogue: lane holds rows m = row0 + wm*WM + 16 i + l16 and, per j, four
         // consecutive columns 16 j + 4 lg + q of the wave's WN-wide column range
         if constexpr (EPI == EPI_PLAIN) {
@@ -378,7 +423,31 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                         const float g = acc[i][j][q], u = acc[i][j + HF][q];
                         h[i][j][q] = g / (1.0f + expf(-g)) * u;
                     }
-            if constexpr (EPI == EPI_SWIGLU_BF16) {
+            if constexpr (EPI == EPI_SWIGLU_F32AMAX) {
+                // fp32 h and the row's max |h| over all of its tiles (atomic max on the float bits:
+                // non-negative floats order like their bit patterns)
+#pragma unroll
+                for (int i = 0; i < IF; ++i) {
+                    const int m = row0 + wm * WM + i * 16 + l16;
+                    float mx = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < HF; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            mx = fmaxf(mx, fabsf(h[i][j][q]));
+                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                    if (m < seg1) {
+                        float *hrow = reinterpret_cast<float *>(p.C) + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
+#pragma unroll
+                        for (int j = 0; j < HF; ++j)
+                            *reinterpret_cast<f32x4 *>(hrow + 16 * j) =
+                                f32x4{h[i][j][0], h[i][j][1], h[i][j][2], h[i][j][3]};
+                        if (lg == 0)
+                            atomicMax(reinterpret_cast<unsigned int *>(p.Cs) + m, __float_as_uint(mx));
+                    }
+                }
+            } else if constexpr (EPI == EPI_SWIGLU_BF16) {
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
                     const int m = row0 + wm * WM + i * 16 + l16;
@@ -541,6 +610,15 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
             return launch_one<DT_BF16, EPI_PLAIN>(a, s);
         if (epi == EPI_SWIGLU_BF16)
             return launch_one<DT_BF16, EPI_SWIGLU_BF16>(a, s);
+    } else if (dt == DT_INT8) {
+        if (epi == EPI_PLAIN)
+            return launch_one<DT_INT8, EPI_PLAIN>(a, s);
+        if (epi == EPI_SWIGLU_F32AMAX) {
+            hipError_t e = launch_fill_i32(reinterpret_cast<int32_t *>(a.Cs), 0, a.M, s);
+            if (e != hipSuccess)
+                return e;
+            return launch_one<DT_INT8, EPI_SWIGLU_F32AMAX>(a, s);
+        }
     } else if (dt == DT_FP8) {
         if (epi == EPI_PLAIN)
             return launch_one<DT_FP8, EPI_PLAIN>(a, s);
@@ -550,6 +628,51 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
             return launch_one<DT_FP8, EPI_SWIGLU_BF16>(a, s);
     }
     return hipErrorInvalidValue;
+}
+
+// Per-token int8 requantisation of h (post_swiglu_dynamic_quant.h:164-231): one block per row.
+__global__ __launch_bounds__(256) void quant_rows_int8_kernel(const float *__restrict__ h,
+                                                              const float *__restrict__ amax_in,
+                                                              const int64_t *__restrict__ group_list, int L, int M,
+                                                              int I, int8_t *__restrict__ q, float *__restrict__ scale)
+{
+    __shared__ int tot;
+    if (threadIdx.x == 0)
+        tot = 0;
+    __syncthreads();
+    int part = 0;
+    for (int e = threadIdx.x; e < L; e += blockDim.x)
+        part += (int)group_list[e];
+    if (part)
+        atomicAdd(&tot, part);
+    __syncthreads();
+    const int total = min(tot, M);
+    for (int m = blockIdx.x; m < total; m += gridDim.x) {
+        const float a = amax_in[m];
+        const float inv = a > 0.0f ? 1.0f / a : 0.0f;  // rows of zeros quantise to 0 with scale 0
+        const f32x4 *hr = reinterpret_cast<const f32x4 *>(h + (size_t)m * I);
+        uint32_t *qr = reinterpret_cast<uint32_t *>(q + (size_t)m * I);
+        for (int c = threadIdx.x; c < I / 4; c += blockDim.x) {
+            const f32x4 v = hr[c];
+            uint32_t pk = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                pk |= (uint32_t)((int)rintf((v[b] * 127.0f) * inv) & 0xff) << (8 * b);
+            qr[c] = pk;
+        }
+        if (threadIdx.x == 0)
+            scale[m] = a * (1.0f / 127.0f);
+    }
+}
+
+hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64_t *group_list, int L, int M, int I,
+                                  int8_t *q, float *scale, hipStream_t s)
+{
+    if (M <= 0 || L <= 0 || (I & 3))
+        return hipErrorInvalidValue;
+    const int grid = M < 4096 ? M : 4096;
+    hipLaunchKernelGGL(quant_rows_int8_kernel, dim3(grid), dim3(256), 0, s, h, amax, group_list, L, M, I, q, scale);
+    return hipGetLastError();
 }
 
 }  // namespace cam

@@ -6,7 +6,8 @@
 
 namespace cam {
 
-enum QuantMode { QUANT_NONE = 0, QUANT_INT8_TOKEN = 2, QUANT_FP8_BLOCK = 3 };
+// QUANT_INT8_FUSED: the fused decode op's int8 recipe (no epsilon, optional smooth scales); internal only
+enum QuantMode { QUANT_NONE = 0, QUANT_INT8_TOKEN = 2, QUANT_FP8_BLOCK = 3, QUANT_INT8_FUSED = 4 };
 
 // ---- routing (route.hip)
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
@@ -43,7 +44,7 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
-                           int32_t *inv_out = nullptr);
+                           int32_t *inv_out = nullptr, const float *smooth = nullptr);
 // combine without the scatter launch, for callers whose dispatch already wrote inv
 hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
                                  const float *topk_w, int T, int K, int H, uint16_t *out, const int32_t *inv,

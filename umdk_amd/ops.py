@@ -202,9 +202,17 @@ def _gmm_common(x, x_scale, group_list, weight, weight_scale, op):
     if x.dtype == torch.bfloat16:
         _check(weight.dtype == torch.bfloat16, f"{op}: bf16 x needs bf16 weight")
         dt = 0
+    elif x.dtype == torch.int8:
+        _check(weight.dtype == torch.int8, f"{op}: int8 x needs int8 weight")
+        _check(x_scale is not None and weight_scale is not None, f"{op}: int8 needs x_scale and weight_scale")
+        _check(x_scale.dtype == torch.float32 and tuple(x_scale.shape) == (x.shape[0],),
+               f"{op}: int8 x_scale must be float32 [m] (per token)")
+        _check(weight_scale.dtype == torch.float32 and tuple(weight_scale.shape) == (L, n),
+               f"{op}: int8 weight_scale must be float32 [groups, n] (per channel)")
+        dt = 2
     else:
         _check(x.dtype == torch.float8_e4m3fn and weight.dtype == torch.float8_e4m3fn,
-               f"{op}: x and weight must both be bfloat16 or both float8_e4m3fn")
+               f"{op}: x and weight must both be bfloat16, int8 or float8_e4m3fn")
         _check(x_scale is not None and weight_scale is not None, f"{op}: fp8 needs x_scale and weight_scale")
         _check(x_scale.dtype == torch.float32 and tuple(x_scale.shape) == (x.shape[0], k // 128),
                f"{op}: x_scale must be float32 [m, k/128]")
@@ -219,11 +227,18 @@ def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quan
     this stage inside fused_deep_moe, grouped_matmul_slice_m_per_token_dequant_
     swiglu_quant_multistage_workspace.h:299-455).  weight [L, 2I, k]: rows
     [0,I) gate, [I,2I) up.  Returns (h [m, I], h_scale): bf16 h and an empty
-    scale for out_quant=0; fp8 h and [m, I/128] scales for out_quant=3."""
+    scale for out_quant=0; fp8 h and [m, I/128] scales for out_quant=3; for int8
+    x and weights (per-token x_scale [m], per-channel weight_scale [L, 2I]),
+    out_quant must be 2: int8 h requantised per token with scales [m]
+    (post_swiglu_dynamic_quant.h:164-231)."""
     dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul_swiglu")
     m = x.shape[0]
     I = n // 2
-    if out_quant == QUANT_FP8_BLOCK:
+    if dt == 2:
+        _check(out_quant == QUANT_INT8_TOKEN, "grouped_matmul_swiglu: int8 inputs need out_quant=2")
+        h = torch.empty((m, I), dtype=torch.int8, device=x.device)
+        hs = torch.empty((m,), dtype=torch.float32, device=x.device)
+    elif out_quant == QUANT_FP8_BLOCK:
         h = torch.empty((m, I), dtype=torch.float8_e4m3fn, device=x.device)
         hs = torch.empty((m, I // 128), dtype=torch.float32, device=x.device)
     else:
@@ -238,7 +253,8 @@ def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quan
 
 def grouped_matmul(x, x_scale, group_list, weight, weight_scale):
     """GMM2 over ragged expert groups: out[m, n] = bf16(x W^T) (addition; the
-    reference's grouped_matmul_slice_m_per_token_dequant_multistage_workspace.h:141-292)."""
+    reference's grouped_matmul_slice_m_per_token_dequant_multistage_workspace.h:141-292).
+    int8: out = bf16(((float)acc * weight_scale[g, n]) * x_scale[m])."""
     dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul")
     m = x.shape[0]
     out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
@@ -276,12 +292,22 @@ def _coupled(ws, L, n, k, what):
 
 
 def _scales(ss, L, n, k, what):
+    """fp8 128x128 block scales [L, n/128, k/128] (one coupled tensor or L per-expert ones)."""
     if not ss or ss[0] is None:
         return None
     s = ss[0] if (len(ss) == 1 and ss[0].dim() == 3) else torch.stack(list(ss))
     _check(s.dtype == torch.float32 and tuple(s.shape) == (L, n // 128, k // 128),
            f"fused_deep_moe: {what} must be float32 [{L}, {n // 128}, {k // 128}] (128x128 block scales)")
     return s.contiguous()
+
+
+def _channel_scales(ss, L, n, what):
+    """int8 per-channel scales [L, n] (coupled) or L tensors of [n]; cast to float32 as the
+    reference's test builds them in float (test_fused_deep_moe.py:309-312)."""
+    _check(bool(ss) and ss[0] is not None, f"fused_deep_moe: int8 weights need {what}")
+    s = ss[0] if (len(ss) == 1 and ss[0].dim() == 2) else torch.stack(list(ss))
+    _check(tuple(s.shape) == (L, n), f"fused_deep_moe: {what} must be [{L}, {n}] per-channel scales")
+    return s.to(torch.float32).contiguous()
 
 
 def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, gmm2_weight_scale, expert_scales,
@@ -296,10 +322,12 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
     [L, H, 2I] / [L, I, H] shapes (one coupled tensor or L separated ones;
     a transposed view of k-contiguous storage avoids a copy), expert_ids
     int32 with -1 placeholders, x_active_mask a true-prefix bool mask.
-    Weights are bf16, or float8_e4m3fn with 128x128 block scales
-    [L, n/128, k/128]; the reference's int8 per-channel weights and the
-    smooth-quant scales are not supported here.  Output shapes are fixed by
-    the inputs, so the op can be captured in a graph."""
+    Weights are int8 with per-channel scales [L, 2I] / [L, H] -- the
+    reference's own mode, with optional smooth-quant scales
+    expert_smooth_scales [moe_expert_num, H] and share_smooth_scales [H] --,
+    bf16, or float8_e4m3fn with 128x128 block scales [L, n/128, k/128].
+    Output shapes are fixed by the inputs, so the op can be captured in a
+    graph."""
     _check(x.dim() == 2 and x.dtype == torch.bfloat16 and x.is_contiguous(),
            "fused_deep_moe: x must be a contiguous [batch, hidden] bfloat16 tensor")
     _check(expert_ids.dim() == 2, "fused_deep_moe: expert_ids must be 2-D")
@@ -308,17 +336,32 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
     k = expert_ids.shape[1]
     L = moe_expert_num // ep_rank_size
     dt = gmm1_weight[0].dtype
-    _check(dt in (torch.bfloat16, torch.float8_e4m3fn),
-           f"fused_deep_moe: weight dtype {dt} not supported (bfloat16 or float8_e4m3fn; int8 per-channel "
-           "weights of the reference are not supported by this build)")
+    _check(dt in (torch.bfloat16, torch.int8, torch.float8_e4m3fn),
+           f"fused_deep_moe: weight dtype {dt} not supported (int8, bfloat16 or float8_e4m3fn)")
     w1_logical = gmm1_weight[0].shape
     n1 = w1_logical[-1]
     I = n1 // 2
     w1 = _coupled(gmm1_weight, L, n1, h, "gmm1_weight")
     w2 = _coupled(gmm2_weight, L, h, I, "gmm2_weight")
     fp8 = dt == torch.float8_e4m3fn
-    s1 = _scales(gmm1_weight_scale, L, n1, h, "gmm1_weight_scale") if fp8 else None
-    s2 = _scales(gmm2_weight_scale, L, h, I, "gmm2_weight_scale") if fp8 else None
+    int8 = dt == torch.int8
+    s1 = s2 = None
+    if fp8:
+        s1 = _scales(gmm1_weight_scale, L, n1, h, "gmm1_weight_scale")
+        s2 = _scales(gmm2_weight_scale, L, h, I, "gmm2_weight_scale")
+    elif int8:
+        s1 = _channel_scales(gmm1_weight_scale, L, n1, "gmm1_weight_scale")
+        s2 = _channel_scales(gmm2_weight_scale, L, h, "gmm2_weight_scale")
+    smooth = share_smooth = None
+    if expert_smooth_scales is not None:
+        _check(int8, "fused_deep_moe: expert_smooth_scales need int8 weights")
+        _check(tuple(expert_smooth_scales.shape) == (moe_expert_num, h),
+               f"fused_deep_moe: expert_smooth_scales must be [{moe_expert_num}, {h}]")
+        smooth = expert_smooth_scales.to(torch.float32).contiguous()
+    if share_smooth_scales is not None and share_gmm1_weight is not None:   # ignored without a shared expert
+        _check(int8, "fused_deep_moe: share_smooth_scales need int8 weights")
+        _check(share_smooth_scales.numel() == h, f"fused_deep_moe: share_smooth_scales must have {h} elements")
+        share_smooth = share_smooth_scales.to(torch.float32).contiguous().view(h)
     shared = share_gmm1_weight is not None
     sw1 = sw2 = ss1 = ss2 = None
     nsh = 0
@@ -330,6 +373,13 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
         if fp8:
             ss1 = share_gmm1_weight_scale.contiguous()
             ss2 = share_gmm2_weight_scale.contiguous()
+        elif int8:
+            _check(share_gmm1_weight_scale is not None and share_gmm2_weight_scale is not None,
+                   "fused_deep_moe: int8 shared expert needs share_gmm1/2_weight_scale")
+            _check(share_gmm1_weight_scale.numel() == nsh and share_gmm2_weight_scale.numel() == h,
+                   f"fused_deep_moe: int8 shared scales must be [{nsh}] and [{h}]")
+            ss1 = share_gmm1_weight_scale.to(torch.float32).contiguous().view(nsh)
+            ss2 = share_gmm2_weight_scale.to(torch.float32).contiguous().view(h)
     ids = expert_ids if expert_ids.dtype == torch.int32 else expert_ids.to(torch.int32)
     ids = ids.contiguous()
     es = expert_scales if expert_scales.dtype == torch.float32 else expert_scales.to(torch.float32)
@@ -342,8 +392,8 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
     etn = torch.empty(L, dtype=torch.int64, device=x.device)
     _lib.call("camhipFusedDeepMoe", _lib.ptr(x), _lib.ptr(ids), _lib.ptr(w1), _lib.ptr(s1), _lib.ptr(w2),
               _lib.ptr(s2), _lib.ptr(es), _lib.ptr(sw1), _lib.ptr(ss1), _lib.ptr(sw2), _lib.ptr(ss2),
-              _lib.ptr(expert_smooth_scales), _lib.ptr(share_smooth_scales), _lib.ptr(mask), bs, h, k, n1, nsh,
-              3 if fp8 else 0, ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs, _lib.ptr(out),
+              _lib.ptr(smooth), _lib.ptr(share_smooth), _lib.ptr(mask), bs, h, k, n1, nsh,
+              3 if fp8 else 2 if int8 else 0, ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs, _lib.ptr(out),
               _lib.ptr(share_out), _lib.ptr(etn), device=x.device)
     return [out, share_out, etn]
 
