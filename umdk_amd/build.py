@@ -20,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
-    # packed fp32 vector ops stay disabled on this pool (build flags)
+    # packed fp32 vector ops stay disabled: some of their forms gave wrong results on this GPU pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-result",
 ]

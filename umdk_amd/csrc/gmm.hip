@@ -39,6 +39,8 @@
 //     groups of 8 M-tiles x all N-tiles (M fastest), remapped so that the
 //     blocks of one XCD take consecutive tiles: they share A and W tiles in
 //     that XCD's L2.
+#include <type_traits>
+
 #include "cam_device.h"
 #include "gmm.h"
 #include "launchers.h"
@@ -137,6 +139,13 @@ template <int N> __device__ __forceinline__ void wait_vmcnt()
 {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt vmcnt(N) and lgkmcnt(0): this wave's older DMAs and all of its LDS reads are done
+template <int N> __device__ __forceinline__ void wait_vmcnt_lgkm0()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4));
 }
 
 // barrier without a memory fence: prefetches in flight stay in flight
@@ -249,20 +258,33 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         for (int d = 0; d < TC::S_DMAS; ++d)
             gs[d] = (uint32_t)min(row0 + wm * WM + d * 64 + lane, p.M - 1) * (uint32_t)nk;
 
-        auto issue = [&](int ks, int slot) {
-            const int kc = min(ks, nk - 1);  // past the end: reload the last k-step (keeps the count uniform)
+        // DMA instruction q (0 <= q < LOADS) of k-step ks into ring slot `slot`: A bands, then W bands,
+        // then (fp8) the activation scales.  Past the end the last k-step is reloaded, which keeps the
+        // number of DMAs per k-step, and so every vmcnt wait, uniform.
+        auto issue_one = [&](int ks, int slot, int q) {
+            const int kc = min(ks, nk - 1);
             uint8_t *st = smem + slot * STAGE_BYTES;
-#pragma unroll
-            for (int i = 0; i < A_LOADS; ++i)
-                dma16(p.A + ga[i] + (uint32_t)kc * GKB, st + (i * NW + w) * 1024);
-#pragma unroll
-            for (int i = 0; i < B_LOADS; ++i)
+            if (q < A_LOADS) {
+                dma16(p.A + ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
+            } else if (q < A_LOADS + B_LOADS) {
+                const int i = q - A_LOADS;
                 dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
-            if constexpr (FP8) {
-#pragma unroll
-                for (int d = 0; d < TC::S_DMAS; ++d)
-                    dma4(p.As + gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            } else {
+                const int d = q - A_LOADS - B_LOADS;
+                dma4(p.As + gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
             }
+        };
+        auto issue = [&](int ks, int slot) {
+#pragma unroll
+            for (int q = 0; q < LOADS; ++q)
+                issue_one(ks, slot, q);
+        };
+        // the DMAs that follow MFMA n of NMF in a phase: spread evenly, so that a wave stalled on a
+        // DMA issue still has MFMAs in the pipe
+        auto issue_after = [&](int n, int nmf, int ks, int slot) {
+#pragma unroll
+            for (int q = n * LOADS / nmf; q < (n + 1) * LOADS / nmf; ++q)
+                issue_one(ks, slot, q);
         };
 
         f32x4 acc[IF][JF];
@@ -287,81 +309,239 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         const float *ws_g = wsc + (SWIGLU ? 0 : ((wn * WN) / 128) * G_MAX_NK);
         const float *ws_u = wsc + G_MAX_NK;
 
+        // ---- main loop, software-pipelined: the LDS->register reads of the next k-step (or half
+        // k-step) are issued before the MFMAs that consume the current one.  Slot ks%STAGES is free
+        // once every wave has read k-step ks into registers, so the DMA of k-step ks+STAGES is issued
+        // right after the barrier that follows those reads.
+        // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
+        // (the DMA of k-step ks+STAGES into slot ks%STAGES is then spread over the next MFMA phase)
+        auto step_edge = [&](int) {
+            wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
+            bar();
+        };
+        auto stage_ptr = [&](int ks) { return smem + (ks % GSTAGES) * STAGE_BYTES; };
+
+        if constexpr (FP8 && BM >= 256) {
+            // 256-row fp8 tile (8 waves of 128 x 64): half the L2->LDS bytes per FLOP of the 128-row
+            // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
+            // W fragments of a k-step read once after the barrier, the A fragments streamed AHEAD rows
+            // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), and
+            // the next k-step's DMA issued during the first half of this k-step's MFMAs.
+            static_assert(GSTAGES == 2, "two-stage ring");
+            constexpr int AHEAD = 2;
+            f32x4 pend[JF];
+            float ps[JF];
 #pragma unroll
-        for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
-            issue(s0, s0);
-        for (int ks = 0; ks < nk; ++ks) {
-            const int cur = ks % GSTAGES;
-            wait_vmcnt<LOADS *(GSTAGES - 2)>();  // this wave's DMA for k-step ks has landed
-            bar();  // ... and every other wave's; the slot of k-step ks-1 is free again
-            issue(ks + GSTAGES - 1, (ks + GSTAGES - 1) % GSTAGES);
-            const uint8_t *st = smem + cur * STAGE_BYTES;
-            const uint8_t *la = st + (wm * WM) * GKB;
-            const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
-            if constexpr (INT8) {
-                // two v_mfma_i32_16x16x64_i8 per k-step; fragments sit where the bf16 ones do
-#pragma unroll
-                for (int sub = 0; sub < 2; ++sub) {
-                    i32x4 afr[IF];
-#pragma unroll
-                    for (int i = 0; i < IF; ++i)
-                        afr[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, sub * 4 + lg));
-#pragma unroll
-                    for (int j = 0; j < JF; ++j) {
-                        const i32x4 bfr = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
-#pragma unroll
-                        for (int i = 0; i < IF; ++i)
-                            acc[i][j] = __builtin_bit_cast(
-                                f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                                           bfr, afr[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
-                    }
-                }
-            } else if constexpr (DT == DT_BF16) {
-#pragma unroll
-                for (int sub = 0; sub < 2; ++sub) {
-                    bf16x8 afr[IF];
-#pragma unroll
-                    for (int i = 0; i < IF; ++i)
-                        afr[i] = *reinterpret_cast<const bf16x8 *>(la + swz(i * 16 + l16, sub * 4 + lg));
-#pragma unroll
-                    for (int j = 0; j < JF; ++j) {
-                        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(lb + swz(j * 16 + l16, sub * 4 + lg));
-#pragma unroll
-                        for (int i = 0; i < IF; ++i)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, afr[i], acc[i][j], 0, 0, 0);
-                    }
-                }
-            } else {
+            for (int j = 0; j < JF; ++j) {
+                pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ps[j] = 0.0f;
+            }
+            issue(0, 0);
+            for (int ks = 0; ks < nk; ++ks) {
+                wait_vmcnt_lgkm0<0>();  // k-step ks has landed; this wave's reads of k-step ks-1 are done
+                bar();                  // ... for every wave: slot (ks+1)%2 is free
+                const uint8_t *st = stage_ptr(ks);
+                const uint8_t *la = st + (wm * WM) * GKB;
+                const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
                 const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4);
-                const float sg = ws_g[ks];
-                const float su = SWIGLU ? ws_u[ks] : sg;
-                // all W fragments of the wave are held; A fragments stream one at a time
-                i32x8 bfr[JF];
+                i32x8 b[JF], a[IF];
+                float sa[IF];
+                auto rd_a = [&](int i) {
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
+                    a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    sa[i] = sst[i * 16 + l16];
+                };
 #pragma unroll
                 for (int j = 0; j < JF; ++j) {
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 2 * lg + 1));
-                    bfr[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                   (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
+                    b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                 }
+                const float sg = ws_g[ks], su = SWIGLU ? ws_u[ks] : sg;
+#pragma unroll
+                for (int i = 0; i < AHEAD; ++i)
+                    rd_a(i);
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
-                    const float sa = sst[i * 16 + l16];
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 2 * lg + 1));
-                    const i32x8 afr = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                            (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    if (i + AHEAD < IF)
+                        rd_a(i + AHEAD);
+                    const float sgi = sa[i] * sg, sui = sa[i] * su;
+                    const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
 #pragma unroll
                     for (int j = 0; j < JF; ++j) {
                         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                         const f32x4 d =
-                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr[j], afr, z, 0, 0, 0, 127, 0, 127);
-                        // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
-                        const float s = sa * ((SWIGLU && j >= JF / 2) ? su : sg);
+                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0, 0, 0, 127, 0, 127);
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
-                            acc[i][j][q] += d[q] * s;
+                            acc[pi][j][q] += pend[j][q] * ps[j];
+                        pend[j] = d;
+                        ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                        const int n = i * JF + j;
+                        if (n < IF * JF / 2)
+                            issue_after(n, IF * JF / 2, ks + 1, (ks + 1) % GSTAGES);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
                     }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < JF; ++j)  // the last row's pending results
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc[IF - 1][j][q] += pend[j][q] * ps[j];
+        } else {
+    #pragma unroll
+            for (int s0 = 0; s0 < GSTAGES; ++s0)
+                issue(s0, s0);
+            wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
+            bar();
+
+            if constexpr (FP8) {
+                // One K=128 MFMA per fragment pair and k-step, and each is one scale block, so its result
+                // is scaled on the VALU.  W fragments are double-buffered; A fragments are refilled row by
+                // row right after the row's MFMAs have issued (one register set plus one W set in flight).
+                // The scaling lags one fragment row behind (row i-1's results are scaled while row i's MFMAs
+                // issue, 4 VALU : 1 MFMA), so the MFMA pipe never waits for a result it has just produced.
+                // A lane's 32 K-bytes are the 16-byte chunks lg and 4+lg of the 128-byte row (not 2lg, 2lg+1):
+                // the same K permutation in both operands leaves each block's dot products unchanged, and
+                // this pattern reads LDS at twice the rate (no 2-way bank conflict).
+                struct WRegs {
+                    i32x8 b[JF];
+                    float sg, su;  // weight scales of the wave's gate / up column blocks
+                };
+                i32x8 a[IF];
+                float sa[IF];  // activation scales of the lane's rows
+                f32x4 pend[JF];
+                float ps[JF];
+    #pragma unroll
+                for (int j = 0; j < JF; ++j) {
+                    pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    ps[j] = 0.0f;
+                }
+                auto rd_w = [&](WRegs &r, int ks) {
+                    const uint8_t *lb = stage_ptr(ks) + A_BYTES + (wn * WN) * GKB;
+    #pragma unroll
+                    for (int j = 0; j < JF; ++j) {
+                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
+                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
+                        r.b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                       (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    }
+                    const int kc = min(ks, nk - 1);
+                    r.sg = ws_g[kc];
+                    r.su = SWIGLU ? ws_u[kc] : r.sg;
+                };
+                auto rd_a = [&](int i, int ks) {
+                    const uint8_t *st = stage_ptr(ks);
+                    const uint8_t *la = st + (wm * WM) * GKB;
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
+                    a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    sa[i] = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4)[i * 16 + l16];
+                };
+                // MFMAs of the k-step held in (a, wr); A rows of k-step ks_next are read behind them and
+                // the DMA of k-step ks_next-1+STAGES is spread between them
+                auto mm = [&](const WRegs &wr, int ks_next) {
+                    const int ks_dma = ks_next - 1 + GSTAGES;
+    #pragma unroll
+                    for (int i = 0; i < IF; ++i) {
+                        const float sgi = sa[i] * wr.sg, sui = sa[i] * wr.su;
+                        const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
+    #pragma unroll
+                        for (int j = 0; j < JF; ++j) {
+                            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                            const f32x4 d =
+                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr.b[j], a[i], z, 0, 0, 0, 127, 0, 127);
+    #pragma unroll
+                            for (int q = 0; q < 4; ++q)
+                                acc[pi][j][q] += pend[j][q] * ps[j];
+                            pend[j] = d;
+                            // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
+                            ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            const int n = i * JF + j;
+                            issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
+                        }
+                        rd_a(i, ks_next);
+                    }
+                };
+                WRegs w0, w1;
+    #pragma unroll
+                for (int i = 0; i < IF; ++i)
+                    rd_a(i, 0);
+                rd_w(w0, 0);
+                int ks = 0;
+                for (; ks + 1 < nk; ks += 2) {
+                    step_edge(ks);
+                    rd_w(w1, ks + 1);
+                    mm(w0, ks + 1);
+                    step_edge(ks + 1);
+                    rd_w(w0, ks + 2);
+                    mm(w1, ks + 2);
+                }
+                if (ks < nk) {
+                    step_edge(ks);
+                    mm(w0, ks + 1);
+                }
+    #pragma unroll
+                for (int j = 0; j < JF; ++j)  // the last row's pending results
+    #pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[IF - 1][j][q] += pend[j][q] * ps[j];
+            } else {
+                // bf16 / int8: two phases per k-step (the K=32 / K=64 halves of the 128-byte step), each
+                // phase's fragments read into the register set the previous phase is not using
+                struct Regs {
+                    i32x4 a[IF];
+                    i32x4 b[JF];
+                };
+                auto rd = [&](Regs &f, int ks, int ph) {
+                    const uint8_t *st = stage_ptr(ks);
+                    const uint8_t *la = st + (wm * WM) * GKB;
+                    const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
+    #pragma unroll
+                    for (int i = 0; i < IF; ++i)
+                        f.a[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, ph * 4 + lg));
+    #pragma unroll
+                    for (int j = 0; j < JF; ++j)
+                        f.b[j] = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, ph * 4 + lg));
+                };
+                // MFMAs of one phase; with ks_dma >= 0 the DMA of that k-step is spread between them
+                auto mm = [&](const Regs &f, int ks_dma) {
+    #pragma unroll
+                    for (int i = 0; i < IF; ++i)
+    #pragma unroll
+                        for (int j = 0; j < JF; ++j) {
+                            if (ks_dma >= 0) {
+                                const int n = i * JF + j;
+                                issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
+                            }
+                            if constexpr (INT8)
+                                acc[i][j] = __builtin_bit_cast(
+                                    f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                               f.b[j], f.a[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
+                            else
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.b[j]),
+                                                                                    __builtin_bit_cast(bf16x8, f.a[i]),
+                                                                                    acc[i][j], 0, 0, 0);
+                        }
+                };
+                Regs r0, r1;
+                rd(r0, 0, 0);
+                for (int ks = 0; ks < nk; ++ks) {
+                    rd(r1, ks, 1);
+                    mm(r0, -1);
+                    step_edge(ks);
+                    rd(r0, ks + 1, 0);
+                    mm(r1, ks + GSTAGES);
                 }
             }
         }
