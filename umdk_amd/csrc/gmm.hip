@@ -227,6 +227,9 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
         const int seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
         const int row0 = seg0 + mt * GBM;
+        // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
+        // DMA and meets every barrier): a tile of a short segment costs little more than its weights
+        const bool wave_active = row0 + wm * WM < seg1;
         const int n0 = SWIGLU ? nt * 128 : nt * GBN;  // first h-column (SwiGLU) or W row (plain)
 
         // ---- per-lane byte offsets of the k-step-0 sources of this wave's DMA bands
@@ -337,6 +340,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                 ps[j] = 0.0f;
             }
             issue(0, 0);
+            auto kloop = [&](auto act) {
             for (int ks = 0; ks < nk; ++ks) {
                 wait_vmcnt_lgkm0<0>();  // k-step ks has landed; this wave's reads of k-step ks-1 are done
                 bar();                  // ... for every wave: slot (ks+1)%2 is free
@@ -372,14 +376,16 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                     const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
 #pragma unroll
                     for (int j = 0; j < JF; ++j) {
-                        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                        const f32x4 d =
-                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0, 0, 0, 127, 0, 127);
+                        if constexpr (decltype(act)::value) {
+                            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                            const f32x4 d =
+                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0, 0, 0, 127, 0, 127);
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            acc[pi][j][q] += pend[j][q] * ps[j];
-                        pend[j] = d;
-                        ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            for (int q = 0; q < 4; ++q)
+                                acc[pi][j][q] += pend[j][q] * ps[j];
+                            pend[j] = d;
+                            ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                        }
                         const int n = i * JF + j;
                         if (n < IF * JF / 2)
                             issue_after(n, IF * JF / 2, ks + 1, (ks + 1) % GSTAGES);
@@ -389,13 +395,18 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                     }
                 }
             }
+            };
+            if (wave_active)
+                kloop(std::true_type{});
+            else
+                kloop(std::false_type{});
 #pragma unroll
             for (int j = 0; j < JF; ++j)  // the last row's pending results
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     acc[IF - 1][j][q] += pend[j][q] * ps[j];
         } else {
-    #pragma unroll
+#pragma unroll
             for (int s0 = 0; s0 < GSTAGES; ++s0)
                 issue(s0, s0);
             wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
@@ -418,14 +429,14 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                 float sa[IF];  // activation scales of the lane's rows
                 f32x4 pend[JF];
                 float ps[JF];
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < JF; ++j) {
                     pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
                     ps[j] = 0.0f;
                 }
                 auto rd_w = [&](WRegs &r, int ks) {
                     const uint8_t *lb = stage_ptr(ks) + A_BYTES + (wn * WN) * GKB;
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < JF; ++j) {
                         const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
                         const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
@@ -447,23 +458,25 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                 };
                 // MFMAs of the k-step held in (a, wr); A rows of k-step ks_next are read behind them and
                 // the DMA of k-step ks_next-1+STAGES is spread between them
-                auto mm = [&](const WRegs &wr, int ks_next) {
+                auto mm = [&](const WRegs &wr, int ks_next, auto act) {
                     const int ks_dma = ks_next - 1 + GSTAGES;
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < IF; ++i) {
                         const float sgi = sa[i] * wr.sg, sui = sa[i] * wr.su;
                         const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
-    #pragma unroll
+#pragma unroll
                         for (int j = 0; j < JF; ++j) {
-                            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                            const f32x4 d =
-                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr.b[j], a[i], z, 0, 0, 0, 127, 0, 127);
-    #pragma unroll
-                            for (int q = 0; q < 4; ++q)
-                                acc[pi][j][q] += pend[j][q] * ps[j];
-                            pend[j] = d;
-                            // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
-                            ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            if constexpr (decltype(act)::value) {
+                                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                                const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr.b[j], a[i], z, 0,
+                                                                                                 0, 0, 127, 0, 127);
+#pragma unroll
+                                for (int q = 0; q < 4; ++q)
+                                    acc[pi][j][q] += pend[j][q] * ps[j];
+                                pend[j] = d;
+                                // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
+                                ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            }
                             const int n = i * JF + j;
                             issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -474,26 +487,32 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                     }
                 };
                 WRegs w0, w1;
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < IF; ++i)
                     rd_a(i, 0);
                 rd_w(w0, 0);
-                int ks = 0;
-                for (; ks + 1 < nk; ks += 2) {
-                    step_edge(ks);
-                    rd_w(w1, ks + 1);
-                    mm(w0, ks + 1);
-                    step_edge(ks + 1);
-                    rd_w(w0, ks + 2);
-                    mm(w1, ks + 2);
-                }
-                if (ks < nk) {
-                    step_edge(ks);
-                    mm(w0, ks + 1);
-                }
-    #pragma unroll
+                auto kloop = [&](auto act) {
+                    int ks = 0;
+                    for (; ks + 1 < nk; ks += 2) {
+                        step_edge(ks);
+                        rd_w(w1, ks + 1);
+                        mm(w0, ks + 1, act);
+                        step_edge(ks + 1);
+                        rd_w(w0, ks + 2);
+                        mm(w1, ks + 2, act);
+                    }
+                    if (ks < nk) {
+                        step_edge(ks);
+                        mm(w0, ks + 1, act);
+                    }
+                };
+                if (wave_active)
+                    kloop(std::true_type{});
+                else
+                    kloop(std::false_type{});
+#pragma unroll
                 for (int j = 0; j < JF; ++j)  // the last row's pending results
-    #pragma unroll
+#pragma unroll
                     for (int q = 0; q < 4; ++q)
                         acc[IF - 1][j][q] += pend[j][q] * ps[j];
             } else {
@@ -507,24 +526,26 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                     const uint8_t *st = stage_ptr(ks);
                     const uint8_t *la = st + (wm * WM) * GKB;
                     const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < IF; ++i)
                         f.a[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, ph * 4 + lg));
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < JF; ++j)
                         f.b[j] = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, ph * 4 + lg));
                 };
                 // MFMAs of one phase; with ks_dma >= 0 the DMA of that k-step is spread between them
-                auto mm = [&](const Regs &f, int ks_dma) {
-    #pragma unroll
+                auto mm = [&](const Regs &f, int ks_dma, auto act) {
+#pragma unroll
                     for (int i = 0; i < IF; ++i)
-    #pragma unroll
+#pragma unroll
                         for (int j = 0; j < JF; ++j) {
                             if (ks_dma >= 0) {
                                 const int n = i * JF + j;
                                 issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
                             }
-                            if constexpr (INT8)
+                            if constexpr (!decltype(act)::value)
+                                ;
+                            else if constexpr (INT8)
                                 acc[i][j] = __builtin_bit_cast(
                                     f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
                                                f.b[j], f.a[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
@@ -536,13 +557,19 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                 };
                 Regs r0, r1;
                 rd(r0, 0, 0);
-                for (int ks = 0; ks < nk; ++ks) {
-                    rd(r1, ks, 1);
-                    mm(r0, -1);
-                    step_edge(ks);
-                    rd(r0, ks + 1, 0);
-                    mm(r1, ks + GSTAGES);
-                }
+                auto kloop = [&](auto act) {
+                    for (int ks = 0; ks < nk; ++ks) {
+                        rd(r1, ks, 1);
+                        mm(r0, -1, act);
+                        step_edge(ks);
+                        rd(r0, ks + 1, 0);
+                        mm(r1, ks + GSTAGES, act);
+                    }
+                };
+                if (wave_active)
+                    kloop(std::true_type{});
+                else
+                    kloop(std::false_type{});
             }
         }
         wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
