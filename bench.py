@@ -26,6 +26,25 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "MoE-layer tokens/s; dispatch+combine HBM GB/s; fp8 grouped-GEMM TFLOPS"
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "dispatch_combine_cfg2_hbm_counters.md")
+
+
+def measured_traffic(kernels):
+    """HBM bytes per launch of `kernels` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+    workload (the table's scaled read + write MB columns), or None when the table is absent."""
+    try:
+        rows = [l.split("|") for l in open(TRAFFIC_PROFILE) if l.startswith("| `")]
+    except OSError:
+        return None
+    total = 0.0
+    for k in kernels:
+        hit = [r for r in rows if k in r[1]]
+        if len(hit) != 1:
+            return None
+        total += (float(hit[0][4]) + float(hit[0][5])) * 1e6
+    return total
+
+
 def dispatch_bytes(T, H, K):
     # read x once; write T*K fp8 rows, their 1x128 scales and the (rank,t,k) triples;
     # read topk ids, send_token_idx and offsets
@@ -356,8 +375,11 @@ def main():
                                "identity experts, bf16 combine)", "tokens": T, "hidden": H, "experts": E,
                    "topk": K, "parallelism": "ep1 (one GPU, no collectives)"},
         "roofline": {"bound": "hbm", "achieved": comb_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": comb_gbps / HBM_PEAK_GBPS, "traffic": None, "kernel": "combine (scatter+gather)",
-                     "algorithmic_bytes": cb},
+                     "frac": comb_gbps / HBM_PEAK_GBPS,
+                     "traffic": measured_traffic(["combine_scatter_kernel", "combine_gather_kernel"]),
+                     "traffic_source": "profiles/dispatch_combine_cfg2_hbm_counters.md (rocprofv3 FETCH_SIZE x2.0 + "
+                                       "WRITE_SIZE x1.0, same workload)",
+                     "kernel": "combine (scatter+gather)", "algorithmic_bytes": cb},
         "dispatch": {"ms": d_ms, "GBps": disp_gbps, "frac": disp_gbps / HBM_PEAK_GBPS, "algorithmic_bytes": db},
         "combine": {"ms": c_ms, "GBps": comb_gbps, "frac": comb_gbps / HBM_PEAK_GBPS},
         "dispatch_combine_GBps": dc_gbps,
