@@ -53,7 +53,6 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
 constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
-constexpr int G_MAX_NK = 128;        // fp8 k <= 16384
 
 // Tile shapes.  BM = 128: 2 x 2 waves of 64 x 128, 3-stage ring (prefill: many rows per expert).
 // BM = 32: 1 x 4 waves of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the
@@ -164,6 +163,21 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
 }
 
+// scalar (SMEM) load of a block-uniform element of read-only data: it counts on lgkmcnt, not on the
+// vmcnt of the DMA ring, so it never makes a wait drain prefetches
+__device__ __forceinline__ float sload(const float *p, int idx)
+{
+    return ((const __attribute__((address_space(4))) float *)p)[idx];
+}
+
+// LDS-only barrier: this wave's LDS traffic has completed, then every wave meets; DMAs in flight stay
+// in flight
+__device__ __forceinline__ void lds_sync()
+{
+    __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0), vmcnt and expcnt at their maxima
+    bar();
+}
+
 template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p)
 {
     using TC = Tile<BM>;
@@ -174,7 +188,6 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
     int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GMAX_THREADS ints: table scan, then the fp8 amax exchange
-    float *wsc = reinterpret_cast<float *>(scratch + 2 * GMAX_THREADS);  // [2][G_MAX_NK] weight scales of the tile
 
     build_group_table<GBM, GTHREADS>(p.group_list, p.L, *gt, scratch);
 
@@ -202,8 +215,15 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     const int band_row = lane >> 3;
     auto chunk_off = [&](int r) { return (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4); };
 
-    for (int tile = logical; tile < total; tile += G) {
-        // ---- tile -> (expert, n-tile, m-tile)
+    // ---- one tile's coordinates and the per-lane sources of this wave's DMA bands
+    struct Ctx {
+        int e, row0, seg1, n0;
+        const uint8_t *wbase;
+        uint32_t ga[A_LOADS], gb[B_LOADS], gs[TC::S_DMAS];
+        int wsg, wsu;  // fp8: weight-scale row offsets (gate / up n-blocks, or the wave's column block)
+        bool active;   // some row of this wave lies inside the segment
+    };
+    auto setup = [&](int tile, Ctx &c) {
         int lo = 0, hi = p.L - 1;
         while (lo < hi) {  // last e with tile_prefix[e]*ntn <= tile
             const int mid = (lo + hi + 1) >> 1;
@@ -212,9 +232,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             else
                 hi = mid - 1;
         }
-        // tile coordinates are block-uniform; say so, so that per-k-step weight-scale loads are
-        // scalar loads and do not share vmcnt with the DMA ring
         const int e = __builtin_amdgcn_readfirstlane(lo);
+        c.e = e;
         const int mt_e = __builtin_amdgcn_readfirstlane(gt->tile_prefix[e + 1] - gt->tile_prefix[e]);
         const int local = __builtin_amdgcn_readfirstlane(tile - gt->tile_prefix[e] * ntn);
         // within the expert: groups of up to 8 M-tiles, N-tiles in turn, the group's M-tiles
@@ -225,20 +244,17 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         const int gm = min(GM, mt_e - grp * GM);
         const int nt = rem / gm, mt = grp * GM + rem % gm;
         const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
-        const int seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
-        const int row0 = seg0 + mt * GBM;
+        c.seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
+        c.row0 = seg0 + mt * GBM;
+        c.n0 = SWIGLU ? nt * 128 : nt * GBN;  // first h-column (SwiGLU) or W row (plain)
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
         // DMA and meets every barrier): a tile of a short segment costs little more than its weights
-        const bool wave_active = row0 + wm * WM < seg1;
-        const int n0 = SWIGLU ? nt * 128 : nt * GBN;  // first h-column (SwiGLU) or W row (plain)
-
-        // ---- per-lane byte offsets of the k-step-0 sources of this wave's DMA bands
-        const uint8_t *wbase = p.W + (size_t)e * p.N * kbytes;
-        uint32_t ga[A_LOADS], gb[B_LOADS];
+        c.active = c.row0 + wm * WM < c.seg1;
+        c.wbase = p.W + (size_t)e * p.N * kbytes;
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
             const int r = (i * NW + w) * 8 + band_row;  // tile row 0..GBM-1
-            ga[i] = (uint32_t)min(row0 + r, p.M - 1) * kbytes + chunk_off(r);
+            c.ga[i] = (uint32_t)min(c.row0 + r, p.M - 1) * kbytes + chunk_off(r);
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
@@ -247,361 +263,43 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             if (SWIGLU) {
                 // LDS rows [WN c, WN c + WN) feed column wave c: WN/2 gate rows, then the
                 // WN/2 up rows of the same h-columns
-                const int c = r / WN, jj = r % WN;
-                const int hcol = n0 + (WN / 2) * c + (jj % (WN / 2));
+                const int cw = r / WN, jj = r % WN;
+                const int hcol = c.n0 + (WN / 2) * cw + (jj % (WN / 2));
                 wrow = jj < WN / 2 ? hcol : half_n + hcol;
             } else {
-                wrow = n0 + r;
+                wrow = c.n0 + r;
             }
-            gb[i] = (uint32_t)wrow * kbytes + chunk_off(r);
+            c.gb[i] = (uint32_t)wrow * kbytes + chunk_off(r);
         }
         // fp8: this wave's activation-scale rows (the WM rows of its row block wm, 64 per DMA)
-        uint32_t gs[TC::S_DMAS];
 #pragma unroll
         for (int d = 0; d < TC::S_DMAS; ++d)
-            gs[d] = (uint32_t)min(row0 + wm * WM + d * 64 + lane, p.M - 1) * (uint32_t)nk;
-
-        // DMA instruction q (0 <= q < LOADS) of k-step ks into ring slot `slot`: A bands, then W bands,
-        // then (fp8) the activation scales.  Past the end the last k-step is reloaded, which keeps the
-        // number of DMAs per k-step, and so every vmcnt wait, uniform.
-        auto issue_one = [&](int ks, int slot, int q) {
-            const int kc = min(ks, nk - 1);
-            uint8_t *st = smem + slot * STAGE_BYTES;
-            if (q < A_LOADS) {
-                dma16(p.A + ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
-            } else if (q < A_LOADS + B_LOADS) {
-                const int i = q - A_LOADS;
-                dma16(wbase + gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
-            } else {
-                const int d = q - A_LOADS - B_LOADS;
-                dma4(p.As + gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
-            }
-        };
-        auto issue = [&](int ks, int slot) {
-#pragma unroll
-            for (int q = 0; q < LOADS; ++q)
-                issue_one(ks, slot, q);
-        };
-        // the DMAs that follow MFMA n of NMF in a phase: spread evenly, so that a wave stalled on a
-        // DMA issue still has MFMAs in the pipe
-        auto issue_after = [&](int n, int nmf, int ks, int slot) {
-#pragma unroll
-            for (int q = n * LOADS / nmf; q < (n + 1) * LOADS / nmf; ++q)
-                issue_one(ks, slot, q);
-        };
-
-        f32x4 acc[IF][JF];
-#pragma unroll
-        for (int i = 0; i < IF; ++i)
-#pragma unroll
-            for (int j = 0; j < JF; ++j)
-                acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-        if constexpr (FP8) {
-            // the tile's weight-scale rows (gate and up n-blocks, or the two 128-column halves)
-            // go to LDS once, so the k-loop issues no vector loads of its own
-            const float *wsb = p.Ws + (size_t)e * (p.N / 128) * nk;
-            const float *r0 = wsb + (size_t)((SWIGLU ? n0 : n0) / 128) * nk;
-            const float *r1 = wsb + (size_t)((SWIGLU ? half_n + n0 : n0 + 128) / 128) * nk;
-            for (int q = tid; q < nk; q += GTHREADS) {
-                wsc[q] = r0[q];
-                wsc[G_MAX_NK + q] = r1[q];
-            }
-            __syncthreads();
-        }
-        const float *ws_g = wsc + (SWIGLU ? 0 : ((wn * WN) / 128) * G_MAX_NK);
-        const float *ws_u = wsc + G_MAX_NK;
-
-        // ---- main loop, software-pipelined: the LDS->register reads of the next k-step (or half
-        // k-step) are issued before the MFMAs that consume the current one.  Slot ks%STAGES is free
-        // once every wave has read k-step ks into registers, so the DMA of k-step ks+STAGES is issued
-        // right after the barrier that follows those reads.
-        // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
-        // (the DMA of k-step ks+STAGES into slot ks%STAGES is then spread over the next MFMA phase)
-        auto step_edge = [&](int) {
-            wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
-            bar();
-        };
-        auto stage_ptr = [&](int ks) { return smem + (ks % GSTAGES) * STAGE_BYTES; };
-
-        if constexpr (FP8 && BM >= 256) {
-            // 256-row fp8 tile (8 waves of 128 x 64): half the L2->LDS bytes per FLOP of the 128-row
-            // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
-            // W fragments of a k-step read once after the barrier, the A fragments streamed AHEAD rows
-            // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), and
-            // the next k-step's DMA issued during the first half of this k-step's MFMAs.
-            static_assert(GSTAGES == 2, "two-stage ring");
-            constexpr int AHEAD = 2;
-            f32x4 pend[JF];
-            float ps[JF];
-#pragma unroll
-            for (int j = 0; j < JF; ++j) {
-                pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-                ps[j] = 0.0f;
-            }
-            issue(0, 0);
-            auto kloop = [&](auto act) {
-            for (int ks = 0; ks < nk; ++ks) {
-                wait_vmcnt_lgkm0<0>();  // k-step ks has landed; this wave's reads of k-step ks-1 are done
-                bar();                  // ... for every wave: slot (ks+1)%2 is free
-                const uint8_t *st = stage_ptr(ks);
-                const uint8_t *la = st + (wm * WM) * GKB;
-                const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
-                const float *sst = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4);
-                i32x8 b[JF], a[IF];
-                float sa[IF];
-                auto rd_a = [&](int i) {
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
-                    a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                    sa[i] = sst[i * 16 + l16];
-                };
-#pragma unroll
-                for (int j = 0; j < JF; ++j) {
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
-                    b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                }
-                const float sg = ws_g[ks], su = SWIGLU ? ws_u[ks] : sg;
-#pragma unroll
-                for (int i = 0; i < AHEAD; ++i)
-                    rd_a(i);
-#pragma unroll
-                for (int i = 0; i < IF; ++i) {
-                    if (i + AHEAD < IF)
-                        rd_a(i + AHEAD);
-                    const float sgi = sa[i] * sg, sui = sa[i] * su;
-                    const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
-#pragma unroll
-                    for (int j = 0; j < JF; ++j) {
-                        if constexpr (decltype(act)::value) {
-                            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                            const f32x4 d =
-                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-                            for (int q = 0; q < 4; ++q)
-                                acc[pi][j][q] += pend[j][q] * ps[j];
-                            pend[j] = d;
-                            ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
-                        }
-                        const int n = i * JF + j;
-                        if (n < IF * JF / 2)
-                            issue_after(n, IF * JF / 2, ks + 1, (ks + 1) % GSTAGES);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
-                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
-                    }
-                }
-            }
-            };
-            if (wave_active)
-                kloop(std::true_type{});
-            else
-                kloop(std::false_type{});
-#pragma unroll
-            for (int j = 0; j < JF; ++j)  // the last row's pending results
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    acc[IF - 1][j][q] += pend[j][q] * ps[j];
+            c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, p.M - 1) * (uint32_t)nk;
+        const int nb = p.N / 128;
+        c.wsg = (e * nb + (SWIGLU ? c.n0 : c.n0 + wn * WN) / 128) * nk;
+        c.wsu = SWIGLU ? (e * nb + (half_n + c.n0) / 128) * nk : c.wsg;
+    };
+    // DMA instruction q (0 <= q < LOADS) of k-step kc of tile c into ring slot `slot`: A bands, then
+    // W bands, then (fp8) the activation scales
+    auto dma_one = [&](const Ctx &c, int kc, int slot, int q) {
+        uint8_t *st = smem + slot * STAGE_BYTES;
+        if (q < A_LOADS) {
+            dma16(p.A + c.ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
+        } else if (q < A_LOADS + B_LOADS) {
+            const int i = q - A_LOADS;
+            dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
         } else {
-#pragma unroll
-            for (int s0 = 0; s0 < GSTAGES; ++s0)
-                issue(s0, s0);
-            wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
-            bar();
-
-            if constexpr (FP8) {
-                // One K=128 MFMA per fragment pair and k-step, and each is one scale block, so its result
-                // is scaled on the VALU.  W fragments are double-buffered; A fragments are refilled row by
-                // row right after the row's MFMAs have issued (one register set plus one W set in flight).
-                // The scaling lags one fragment row behind (row i-1's results are scaled while row i's MFMAs
-                // issue, 4 VALU : 1 MFMA), so the MFMA pipe never waits for a result it has just produced.
-                // A lane's 32 K-bytes are the 16-byte chunks lg and 4+lg of the 128-byte row (not 2lg, 2lg+1):
-                // the same K permutation in both operands leaves each block's dot products unchanged, and
-                // this pattern reads LDS at twice the rate (no 2-way bank conflict).
-                struct WRegs {
-                    i32x8 b[JF];
-                    float sg, su;  // weight scales of the wave's gate / up column blocks
-                };
-                i32x8 a[IF];
-                float sa[IF];  // activation scales of the lane's rows
-                f32x4 pend[JF];
-                float ps[JF];
-#pragma unroll
-                for (int j = 0; j < JF; ++j) {
-                    pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    ps[j] = 0.0f;
-                }
-                auto rd_w = [&](WRegs &r, int ks) {
-                    const uint8_t *lb = stage_ptr(ks) + A_BYTES + (wn * WN) * GKB;
-#pragma unroll
-                    for (int j = 0; j < JF; ++j) {
-                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
-                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
-                        r.b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                       (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                    }
-                    const int kc = min(ks, nk - 1);
-                    r.sg = ws_g[kc];
-                    r.su = SWIGLU ? ws_u[kc] : r.sg;
-                };
-                auto rd_a = [&](int i, int ks) {
-                    const uint8_t *st = stage_ptr(ks);
-                    const uint8_t *la = st + (wm * WM) * GKB;
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
-                    a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
-                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                    sa[i] = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4)[i * 16 + l16];
-                };
-                // MFMAs of the k-step held in (a, wr); A rows of k-step ks_next are read behind them and
-                // the DMA of k-step ks_next-1+STAGES is spread between them
-                auto mm = [&](const WRegs &wr, int ks_next, auto act) {
-                    const int ks_dma = ks_next - 1 + GSTAGES;
-#pragma unroll
-                    for (int i = 0; i < IF; ++i) {
-                        const float sgi = sa[i] * wr.sg, sui = sa[i] * wr.su;
-                        const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
-#pragma unroll
-                        for (int j = 0; j < JF; ++j) {
-                            if constexpr (decltype(act)::value) {
-                                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                                const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr.b[j], a[i], z, 0,
-                                                                                                 0, 0, 127, 0, 127);
-#pragma unroll
-                                for (int q = 0; q < 4; ++q)
-                                    acc[pi][j][q] += pend[j][q] * ps[j];
-                                pend[j] = d;
-                                // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
-                                ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
-                            }
-                            const int n = i * JF + j;
-                            issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
-                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
-                            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
-                        }
-                        rd_a(i, ks_next);
-                    }
-                };
-                WRegs w0, w1;
-#pragma unroll
-                for (int i = 0; i < IF; ++i)
-                    rd_a(i, 0);
-                rd_w(w0, 0);
-                auto kloop = [&](auto act) {
-                    int ks = 0;
-                    for (; ks + 1 < nk; ks += 2) {
-                        step_edge(ks);
-                        rd_w(w1, ks + 1);
-                        mm(w0, ks + 1, act);
-                        step_edge(ks + 1);
-                        rd_w(w0, ks + 2);
-                        mm(w1, ks + 2, act);
-                    }
-                    if (ks < nk) {
-                        step_edge(ks);
-                        mm(w0, ks + 1, act);
-                    }
-                };
-                if (wave_active)
-                    kloop(std::true_type{});
-                else
-                    kloop(std::false_type{});
-#pragma unroll
-                for (int j = 0; j < JF; ++j)  // the last row's pending results
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        acc[IF - 1][j][q] += pend[j][q] * ps[j];
-            } else {
-                // bf16 / int8: two phases per k-step (the K=32 / K=64 halves of the 128-byte step), each
-                // phase's fragments read into the register set the previous phase is not using
-                struct Regs {
-                    i32x4 a[IF];
-                    i32x4 b[JF];
-                };
-                auto rd = [&](Regs &f, int ks, int ph) {
-                    const uint8_t *st = stage_ptr(ks);
-                    const uint8_t *la = st + (wm * WM) * GKB;
-                    const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
-#pragma unroll
-                    for (int i = 0; i < IF; ++i)
-                        f.a[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, ph * 4 + lg));
-#pragma unroll
-                    for (int j = 0; j < JF; ++j)
-                        f.b[j] = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, ph * 4 + lg));
-                };
-                // MFMAs of one phase; with ks_dma >= 0 the DMA of that k-step is spread between them
-                auto mm = [&](const Regs &f, int ks_dma, auto act) {
-#pragma unroll
-                    for (int i = 0; i < IF; ++i)
-#pragma unroll
-                        for (int j = 0; j < JF; ++j) {
-                            if (ks_dma >= 0) {
-                                const int n = i * JF + j;
-                                issue_after(n, IF * JF, ks_dma, ks_dma % GSTAGES);
-                            }
-                            if constexpr (!decltype(act)::value)
-                                ;
-                            else if constexpr (INT8)
-                                acc[i][j] = __builtin_bit_cast(
-                                    f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                                               f.b[j], f.a[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
-                            else
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.b[j]),
-                                                                                    __builtin_bit_cast(bf16x8, f.a[i]),
-                                                                                    acc[i][j], 0, 0, 0);
-                        }
-                };
-                Regs r0, r1;
-                rd(r0, 0, 0);
-                auto kloop = [&](auto act) {
-                    for (int ks = 0; ks < nk; ++ks) {
-                        rd(r1, ks, 1);
-                        mm(r0, -1, act);
-                        step_edge(ks);
-                        rd(r0, ks + 1, 0);
-                        mm(r1, ks + GSTAGES, act);
-                    }
-                };
-                if (wave_active)
-                    kloop(std::true_type{});
-                else
-                    kloop(std::false_type{});
-            }
+            const int d = q - A_LOADS - B_LOADS;
+            dma4(p.As + c.gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
         }
-        wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
-        bar();
+    };
 
-        if constexpr (INT8) {
-            // per-channel x per-token dequantisation of the exact int32 sums:
-            // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
-            const float *wsr = p.Ws + (size_t)e * p.N;
-#pragma unroll
-            for (int j = 0; j < JF; ++j) {
-                int c0;
-                if (SWIGLU) {
-                    const int jj = j % (JF / 2);
-                    c0 = n0 + (WN / 2) * wn + 16 * jj + 4 * lg + (j >= JF / 2 ? half_n : 0);
-                } else {
-                    c0 = n0 + wn * WN + 16 * j + 4 * lg;
-                }
-                const f32x4 wv = *reinterpret_cast<const f32x4 *>(wsr + c0);
-#pragma unroll
-                for (int i = 0; i < IF; ++i) {
-                    const float xs = p.As[min(row0 + wm * WM + i * 16 + l16, p.M - 1)];
-                    const i32x4 iv = __builtin_bit_cast(i32x4, acc[i][j]);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        acc[i][j][q] = ((float)iv[q] * wv[q]) * xs;
-                }
-            }
-        }
+    f32x4 acc[IF][JF];
 
-        // ---- epilogue: lane holds rows m = row0 + wm*WM + 16 i + l16 and, per j, four
-        // consecutive columns 16 j + 4 lg + q of the wave's WN-wide column range
+    // ---- epilogue: lane holds rows m = row0 + wm*WM + 16 i + l16 and, per j, four
+    // consecutive columns 16 j + 4 lg + q of the wave's WN-wide column range
+    auto epilogue = [&](const Ctx &c) {
+        const int row0 = c.row0, seg1 = c.seg1, n0 = c.n0;
         if constexpr (EPI == EPI_PLAIN) {
 #pragma unroll
             for (int i = 0; i < IF; ++i) {
@@ -687,15 +385,15 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                     if (lg == 0)
                         red[wn * GBM + wm * WM + i * 16 + l16] = mx;
                 }
-                __syncthreads();
+                lds_sync();
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
                     const int r = wm * WM + i * 16 + l16;
                     const int m = row0 + r;
                     float amax = 1e-4f;
 #pragma unroll
-                    for (int c = 0; c < TC::WAVES_N; ++c)
-                        amax = fmaxf(amax, red[c * GBM + r]);
+                    for (int cc = 0; cc < TC::WAVES_N; ++cc)
+                        amax = fmaxf(amax, red[cc * GBM + r]);
                     const float inv = 448.0f / amax;
                     if (m < seg1) {
                         uint8_t *hrow = p.C + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
@@ -707,9 +405,366 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                             p.Cs[(size_t)m * (half_n / 128) + n0 / 128] = amax / 448.0f;
                     }
                 }
-                __syncthreads();  // red is reused by the next tile
+                lds_sync();  // red is reused by the next tile
             }
         }
+    };
+    auto clear_acc = [&]() {
+#pragma unroll
+        for (int i = 0; i < IF; ++i)
+#pragma unroll
+            for (int j = 0; j < JF; ++j)
+                acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    if constexpr (FP8 && BM >= 256) {
+        // 256-row fp8 tile (8 waves of 128 x 64): half the L2->LDS bytes per FLOP of the 128-row
+        // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
+        // W fragments of a k-step read once after the barrier, the A fragments streamed AHEAD rows
+        // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), and
+        // the next k-step's DMA issued during the first half of this k-step's MFMAs.  Tiles do not
+        // overlap: each starts with its own first DMA and drains at its end.
+        static_assert(GSTAGES == 2, "two-stage ring");
+        constexpr int AHEAD = 2;
+        for (int tile = logical; tile < total; tile += G) {
+            Ctx c;
+            setup(tile, c);
+            clear_acc();
+            f32x4 pend[JF];
+            float ps[JF];
+#pragma unroll
+            for (int j = 0; j < JF; ++j) {
+                pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ps[j] = 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < LOADS; ++q)
+                dma_one(c, 0, 0, q);
+            auto kloop = [&](auto act) {
+                for (int ks = 0; ks < nk; ++ks) {
+                    wait_vmcnt_lgkm0<0>();  // k-step ks has landed; this wave's reads of k-step ks-1 are done
+                    bar();                  // ... for every wave: slot (ks+1)%2 is free
+                    const uint8_t *st = smem + (ks & 1) * STAGE_BYTES;
+                    const uint8_t *la = st + (wm * WM) * GKB;
+                    const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
+                    const float *sst =
+                        reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4);
+                    i32x8 b[JF], a[IF];
+                    float sa[IF];
+                    auto rd_a = [&](int i) {
+                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
+                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
+                        a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                     (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                        sa[i] = sst[i * 16 + l16];
+                    };
+#pragma unroll
+                    for (int j = 0; j < JF; ++j) {
+                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
+                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
+                        b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                     (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    }
+                    const float sg = sload(p.Ws, c.wsg + ks), su = SWIGLU ? sload(p.Ws, c.wsu + ks) : sg;
+                    const int kn = min(ks + 1, nk - 1);  // past the end: reload the last k-step
+#pragma unroll
+                    for (int i = 0; i < AHEAD; ++i)
+                        rd_a(i);
+#pragma unroll
+                    for (int i = 0; i < IF; ++i) {
+                        if (i + AHEAD < IF)
+                            rd_a(i + AHEAD);
+                        const float sgi = sa[i] * sg, sui = sa[i] * su;
+                        const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
+#pragma unroll
+                        for (int j = 0; j < JF; ++j) {
+                            if constexpr (decltype(act)::value) {
+                                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                                const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0,
+                                                                                                 0, 0, 127, 0, 127);
+#pragma unroll
+                                for (int q = 0; q < 4; ++q)
+                                    acc[pi][j][q] += pend[j][q] * ps[j];
+                                pend[j] = d;
+                                ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            }
+                            const int n = i * JF + j;
+                            if (n < IF * JF / 2) {
+#pragma unroll
+                                for (int q = n * LOADS / (IF * JF / 2); q < (n + 1) * LOADS / (IF * JF / 2); ++q)
+                                    dma_one(c, kn, (ks + 1) & 1, q);
+                            }
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
+                        }
+                    }
+                }
+            };
+            if (c.active)
+                kloop(std::true_type{});
+            else
+                kloop(std::false_type{});
+#pragma unroll
+            for (int j = 0; j < JF; ++j)  // the last row's pending results
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc[IF - 1][j][q] += pend[j][q] * ps[j];
+            wait_vmcnt<0>();  // the tail's reload has landed before the next tile reuses the ring
+            bar();
+            epilogue(c);
+        }
+        return;
+    } else {
+        // ---- 128/32-row tiles: software-pipelined k-loop over a ring of STAGES slots, continued
+        // across the block's tiles.  Ring slots are indexed by the block's running k-step count kb+ks,
+        // and the DMA of k-step ks+STAGES is spread over the MFMAs of k-step ks (or of its second
+        // half); past the end of a tile it fetches the next tile's first k-steps, so a tile starts
+        // with its operands already in flight.  With fewer k-steps than stages, or no next tile, the
+        // past-the-end DMAs reload the tile's last k-step (the DMA count per k-step, and so every
+        // vmcnt wait, stays uniform) and the ring is drained before the next tile.
+        int tile = logical;
+        if (tile >= total)
+            return;
+        Ctx cur, nxt;
+        setup(tile, cur);
+        int kb = 0;          // the block's k-steps before the current tile
+        bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
+        while (true) {
+            const int ntile = tile + G;
+            const bool has_next = ntile < total;
+            // (int8: the dequantisation's vector loads would wait for the next tile's DMAs, so no chaining)
+            const bool chain = !INT8 && has_next && nk >= GSTAGES;
+            if (has_next)
+                setup(ntile, nxt);
+            else
+                nxt = cur;
+            auto slot = [&](int ks) { return (kb + ks) % GSTAGES; };
+            auto stage_ptr = [&](int ks) { return smem + slot(ks) * STAGE_BYTES; };
+            // DMA instruction q of the current tile's k-step ksx (ksx may run past the end)
+            auto dma_ks = [&](int ksx, int q) {
+                const bool in = ksx < nk;
+                const Ctx &c = (!in && chain) ? nxt : cur;
+                const int kc = in ? ksx : (chain ? ksx - nk : nk - 1);
+                dma_one(c, kc, slot(ksx), q);
+            };
+            // the DMAs that follow MFMA n of NMF in a phase: spread evenly, so that a wave stalled on
+            // a DMA issue still has MFMAs in the pipe
+            auto dma_after = [&](int n, int nmf, int ksx) {
+#pragma unroll
+                for (int q = n * LOADS / nmf; q < (n + 1) * LOADS / nmf; ++q)
+                    dma_ks(ksx, q);
+            };
+            if (!primed) {
+#pragma unroll
+                for (int s0 = 0; s0 < GSTAGES; ++s0)
+#pragma unroll
+                    for (int q = 0; q < LOADS; ++q)
+                        dma_one(cur, min(s0, nk - 1), slot(s0), q);
+            }
+            wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
+            bar();
+            clear_acc();
+            // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
+            auto step_edge = [&]() {
+                wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
+                bar();
+            };
+
+            if constexpr (FP8) {
+                // One K=128 MFMA per fragment pair and k-step, and each is one scale block, so its result
+                // is scaled on the VALU.  W fragments are double-buffered; A fragments are refilled row by
+                // row right after the row's MFMAs have issued (one register set plus one W set in flight).
+                // The scaling lags one fragment row behind (row i-1's results are scaled while row i's MFMAs
+                // issue, 4 VALU : 1 MFMA), so the MFMA pipe never waits for a result it has just produced.
+                // A lane's 32 K-bytes are the 16-byte chunks lg and 4+lg of the 128-byte row (not 2lg, 2lg+1):
+                // the same K permutation in both operands leaves each block's dot products unchanged, and
+                // this pattern reads LDS at twice the rate (no 2-way bank conflict).
+                struct WRegs {
+                    i32x8 b[JF];
+                    float sg, su;  // weight scales of the wave's gate / up column blocks
+                };
+                i32x8 a[IF];
+                float sa[IF];  // activation scales of the lane's rows
+                f32x4 pend[JF];
+                float ps[JF];
+#pragma unroll
+                for (int j = 0; j < JF; ++j) {
+                    pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    ps[j] = 0.0f;
+                }
+                auto rd_w = [&](WRegs &r, int ks) {
+                    const uint8_t *lb = stage_ptr(ks) + A_BYTES + (wn * WN) * GKB;
+#pragma unroll
+                    for (int j = 0; j < JF; ++j) {
+                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, lg));
+                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(lb + swz(j * 16 + l16, 4 + lg));
+                        r.b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                       (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    }
+                    const int kc = min(ks, nk - 1);
+                    r.sg = sload(p.Ws, cur.wsg + kc);
+                    r.su = SWIGLU ? sload(p.Ws, cur.wsu + kc) : r.sg;
+                };
+                auto rd_a = [&](int i, int ks) {
+                    const uint8_t *st = stage_ptr(ks);
+                    const uint8_t *la = st + (wm * WM) * GKB;
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, lg));
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
+                    a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                                 (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+                    sa[i] = reinterpret_cast<const float *>(st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4)[i * 16 + l16];
+                };
+                // MFMAs of the k-step held in (a, wr); A rows of k-step ks_next are read behind them and
+                // the DMA of k-step ks_next-1+STAGES is spread between them
+                auto mm = [&](const WRegs &wr, int ks_next, auto act) {
+                    const int ks_dma = ks_next - 1 + GSTAGES;
+#pragma unroll
+                    for (int i = 0; i < IF; ++i) {
+                        const float sgi = sa[i] * wr.sg, sui = sa[i] * wr.su;
+                        const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
+#pragma unroll
+                        for (int j = 0; j < JF; ++j) {
+                            if constexpr (decltype(act)::value) {
+                                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                                const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr.b[j], a[i], z, 0,
+                                                                                                 0, 0, 127, 0, 127);
+#pragma unroll
+                                for (int q = 0; q < 4; ++q)
+                                    acc[pi][j][q] += pend[j][q] * ps[j];
+                                pend[j] = d;
+                                // in SwiGLU tiles a wave's columns j < JF/2 are gate rows, the rest up rows
+                                ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
+                            }
+                            dma_after(i * JF + j, IF * JF, ks_dma);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
+                        }
+                        rd_a(i, ks_next);
+                    }
+                };
+                WRegs w0, w1;
+#pragma unroll
+                for (int i = 0; i < IF; ++i)
+                    rd_a(i, 0);
+                rd_w(w0, 0);
+                auto kloop = [&](auto act) {
+                    int ks = 0;
+                    for (; ks + 1 < nk; ks += 2) {
+                        step_edge();
+                        rd_w(w1, ks + 1);
+                        mm(w0, ks + 1, act);
+                        step_edge();
+                        rd_w(w0, ks + 2);
+                        mm(w1, ks + 2, act);
+                    }
+                    if (ks < nk) {
+                        step_edge();
+                        mm(w0, ks + 1, act);
+                    }
+                };
+                if (cur.active)
+                    kloop(std::true_type{});
+                else
+                    kloop(std::false_type{});
+#pragma unroll
+                for (int j = 0; j < JF; ++j)  // the last row's pending results
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[IF - 1][j][q] += pend[j][q] * ps[j];
+            } else {
+                // bf16 / int8: two phases per k-step (the K=32 / K=64 halves of the 128-byte step), each
+                // phase's fragments read into the register set the previous phase is not using
+                struct Regs {
+                    i32x4 a[IF];
+                    i32x4 b[JF];
+                };
+                auto rd = [&](Regs &f, int ks, int ph) {
+                    const uint8_t *st = stage_ptr(ks);
+                    const uint8_t *la = st + (wm * WM) * GKB;
+                    const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
+#pragma unroll
+                    for (int i = 0; i < IF; ++i)
+                        f.a[i] = *reinterpret_cast<const i32x4 *>(la + swz(i * 16 + l16, ph * 4 + lg));
+#pragma unroll
+                    for (int j = 0; j < JF; ++j)
+                        f.b[j] = *reinterpret_cast<const i32x4 *>(lb + swz(j * 16 + l16, ph * 4 + lg));
+                };
+                // MFMAs of one phase; with ks_dma >= 0 the DMA of that k-step is spread between them
+                auto mm = [&](const Regs &f, int ks_dma, auto act) {
+#pragma unroll
+                    for (int i = 0; i < IF; ++i)
+#pragma unroll
+                        for (int j = 0; j < JF; ++j) {
+                            if (ks_dma >= 0)
+                                dma_after(i * JF + j, IF * JF, ks_dma);
+                            if constexpr (!decltype(act)::value)
+                                ;
+                            else if constexpr (INT8)
+                                acc[i][j] = __builtin_bit_cast(
+                                    f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                               f.b[j], f.a[i], __builtin_bit_cast(i32x4, acc[i][j]), 0, 0, 0));
+                            else
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.b[j]),
+                                                                                    __builtin_bit_cast(bf16x8, f.a[i]),
+                                                                                    acc[i][j], 0, 0, 0);
+                        }
+                };
+                Regs r0, r1;
+                rd(r0, 0, 0);
+                auto kloop = [&](auto act) {
+                    for (int ks = 0; ks < nk; ++ks) {
+                        rd(r1, ks, 1);
+                        mm(r0, -1, act);
+                        step_edge();
+                        rd(r0, ks + 1, 0);
+                        mm(r1, ks + GSTAGES, act);
+                    }
+                };
+                if (cur.active)
+                    kloop(std::true_type{});
+                else
+                    kloop(std::false_type{});
+            }
+
+            if constexpr (INT8) {
+                // per-channel x per-token dequantisation of the exact int32 sums:
+                // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
+                const float *wsr = p.Ws + (size_t)cur.e * p.N;
+#pragma unroll
+                for (int j = 0; j < JF; ++j) {
+                    int c0;
+                    if (SWIGLU) {
+                        const int jj = j % (JF / 2);
+                        c0 = cur.n0 + (WN / 2) * wn + 16 * jj + 4 * lg + (j >= JF / 2 ? half_n : 0);
+                    } else {
+                        c0 = cur.n0 + wn * WN + 16 * j + 4 * lg;
+                    }
+                    const f32x4 wv = *reinterpret_cast<const f32x4 *>(wsr + c0);
+#pragma unroll
+                    for (int i = 0; i < IF; ++i) {
+                        const float xs = p.As[min(cur.row0 + wm * WM + i * 16 + l16, p.M - 1)];
+                        const i32x4 iv = __builtin_bit_cast(i32x4, acc[i][j]);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[i][j][q] = ((float)iv[q] * wv[q]) * xs;
+                    }
+                }
+            }
+            if (!chain) {
+                wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
+                bar();
+            }
+            epilogue(cur);
+            kb += nk;
+            if (!has_next)
+                break;
+            primed = chain;
+            tile = ntile;
+            cur = nxt;
+        }
+        wait_vmcnt<0>();  // every DMA has landed before the block exits
     }
 }
 
@@ -751,8 +806,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
 
 template <int BM> constexpr size_t lds_bytes()
 {
-    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int) +
-           2 * G_MAX_NK * sizeof(float);
+    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int);
 }
 static_assert(lds_bytes<32>() <= 163840 && lds_bytes<128>() <= 163840 && lds_bytes<256>() <= 163840,
               "LDS budget of a gfx950 workgroup");
