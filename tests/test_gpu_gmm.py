@@ -207,3 +207,8 @@ def test_gmm_long_segments_take_256_row_tile(ops, dtype):
 def test_gmm_short_segments_in_large_capacity_take_128_row_tile(ops, dtype):
     # a 4096-row capacity (prefill-sized) holding 45 rows: the device picks the 128-row tile over the 256-row one
     _ragged_vs_torch(ops, [10, 0, 30, 5], 1024, 256, dtype, 4096 - 45, 22)
+
+
+def test_gmm_fp8_long_reduction(ops):
+    # k = 17408 (136 k-steps, past any per-tile staging of the weight scales)
+    _ragged_vs_torch(ops, [40, 3], 17408, 128, "fp8", 0, 24)

@@ -134,8 +134,6 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             "fused_deep_moe: hidden %lld must be in [1024,7168] and a multiple of 256", (long long)hidden);
     F_CHECK(gmm1HiddenSize >= 256 && gmm1HiddenSize % 256 == 0,
             "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
-    F_CHECK(weightDtype != CAMHIP_DTYPE_FP8 || (gmm1HiddenSize / 2 <= 16384 && shareGmm1HiddenSize / 2 <= 16384),
-            "fused_deep_moe: fp8 intermediate sizes above 16384 are not supported");
     F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_INT8 || weightDtype == CAMHIP_DTYPE_FP8,
             "fused_deep_moe: weight dtype %lld not supported (bf16, int8 or fp8 e4m3fn)", (long long)weightDtype);
     F_CHECK(quantMode == 0, "fused_deep_moe: quant_mode is reserved and must be 0 (got %lld)", (long long)quantMode);
