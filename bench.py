@@ -73,7 +73,7 @@ def cpu_baseline(T, H, E, K, seed):
         ex, sc, eidx = orc.dispatch(x, idx, so, sti, E, orc.QUANT_FP8)
         orc.combine(y, eidx, idx, w, E)
         reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 3:
+        if time.perf_counter() - t0 > 10.0:  # a bounded ~10 s sample of CPU work
             break
     dt = (time.perf_counter() - t0) / reps
     return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
