@@ -94,13 +94,19 @@ def zipf_bias(E, s, seed):
 
 
 def make_weights(L, H, I, dtype, dev, seed):
-    """W1 [L, 2I, H], W2 [L, H, I] ~ N(0, 0.02); fp8: 128x128 block-quantised e4m3fn + fp32 scales."""
+    """W1 [L, 2I, H], W2 [L, H, I] ~ N(0, 0.02); fp8: 128x128 block-quantised e4m3fn + fp32 scales;
+    int8: per-output-channel symmetric int8 + fp32 scales [L, n] (the reference's fused-op weights)."""
     g = torch.Generator(device=dev).manual_seed(seed + 5)
 
     def one(shape):
         w = torch.randn(shape, device=dev, generator=g, dtype=torch.float32) * 0.02
         if dtype == "bf16":
             return w.bfloat16(), None
+        if dtype == "int8":
+            sc = w.abs().amax(dim=2).clamp(min=1e-6) / 127.0
+            q = torch.round(w / sc[:, :, None]).clamp(-127, 127).to(torch.int8)
+            del w
+            return q, sc.contiguous()
         Ln, n, k = shape
         wv = w.view(Ln, n // 128, 128, k // 128, 128)
         amax = wv.abs().amax(dim=(2, 4)).clamp(min=1e-6)
@@ -209,9 +215,10 @@ def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536)):
     return out
 
 
-def run_decode(steps, seed):
+def run_decode(steps, seed, dtype="fp8"):
     """Config 5: decode step (T=128, H=7168, route over 256 experts, 32 local experts, I=2048, fp8)
-    = route + fused_deep_moe captured in one HIP graph; p50/p99 of single-replay times."""
+    = route + fused_deep_moe captured in one HIP graph; p50/p99 of single-replay times.  dtype "int8"
+    runs the same step with the reference's int8 W8A8 weights (per-channel scales)."""
     import numpy as np
 
     from umdk_amd import _lib
@@ -220,14 +227,15 @@ def run_decode(steps, seed):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(T, H, generator=g).bfloat16().to(dev)
     logits = torch.randn(T, E, generator=g).to(dev)
-    w1, s1, w2, s2 = make_weights(L, H, I, "fp8", dev, seed)
+    w1, s1, w2, s2 = make_weights(L, H, I, dtype, dev, seed)
     ids = torch.empty(T, K, dtype=torch.int32, device=dev)
     wts = torch.empty(T, K, dtype=torch.float32, device=dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     share = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     etn = torch.empty(L, dtype=torch.int64, device=dev)
     fargs = (x.data_ptr(), ids.data_ptr(), w1.data_ptr(), s1.data_ptr(), w2.data_ptr(), s2.data_ptr(),
-             wts.data_ptr(), None, None, None, None, None, None, None, T, H, K, 2 * I, 0, 3, 1, 0, L, 0, 0,
+             wts.data_ptr(), None, None, None, None, None, None, None, T, H, K, 2 * I, 0, 3 if dtype == "fp8" else 2,
+             1, 0, L, 0, 0,
              out.data_ptr(), share.data_ptr(), etn.data_ptr())
     ws = torch.empty(_lib.workspace_size("camhipFusedDeepMoe", *fargs), dtype=torch.uint8, device=dev)
 
@@ -260,9 +268,9 @@ def run_decode(steps, seed):
     times = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
     counts = etn.cpu()
     touched = int((counts > 0).sum())
-    wbytes = touched * 3 * H * I   # fp8 W1 (2I x H) + W2 (H x I) of touched experts
+    wbytes = touched * 3 * H * I   # 1-byte W1 (2I x H) + W2 (H x I) of touched experts
     p50 = float(np.percentile(times, 50))
-    return {"workload": "config5: decode step, route + fused_deep_moe in one HIP graph, fp8", "tokens": T,
+    return {"workload": f"config5: decode step, route + fused_deep_moe in one HIP graph, {dtype}", "tokens": T,
             "hidden": H, "experts_routed": E, "local_experts": L, "topk": K, "intermediate": I,
             "replays": steps, "p50_us": p50, "p99_us": float(np.percentile(times, 99)),
             "mean_us": float(times.mean()), "local_rows": int(counts.sum()), "experts_touched": touched,
@@ -277,9 +285,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "sweep", "all"],
+    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "5i8", "sweep", "all"],
                     help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
-                         "3/4/5: only that config; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
+                         "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
     ap.add_argument("--sweep-m", type=int, default=0, help="--config sweep: only this M")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
@@ -304,9 +312,10 @@ def main():
                                     "bf16", st, wu, args.seed, None)
     cfg4 = lambda st, wu: run_layer("config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), fp8",
                                     4096, 7168, 256, 8, 32, 2048, "fp8", st, wu, args.seed, "zipf")
-    if args.config in ("3", "4", "5", "sweep"):
+    if args.config in ("3", "4", "5", "5i8", "sweep"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed),
+             "5i8": lambda: run_decode(max(args.steps, 1000), args.seed, "int8"),
              "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
                                          (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536))
              }[args.config]()
@@ -393,6 +402,8 @@ def main():
         result["config4"] = cfg4(20, 5)
         torch.cuda.empty_cache()
         result["config5"] = run_decode(1000, args.seed)
+        torch.cuda.empty_cache()
+        result["config5_int8"] = run_decode(1000, args.seed, "int8")
         torch.cuda.empty_cache()
     if args.config == "all":
         result["fp8_gemm_sweep"] = gemm_sweep(10, 3, args.seed)
