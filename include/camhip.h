@@ -117,6 +117,10 @@ CAMHIP_API camhipStatus camhipNotifyDispatch(void *workspace, uint64_t workspace
  * recvRowsCapacity.  recvX [rows, hidden]: bf16 (quantMode 0), int8 (2) or
  * fp8 e4m3fn (3).  recvXScales: untouched (0), [rows] (2), [rows, hidden/128] (3).
  * assistInfoForCombine [rows, 3] int32 = (epRankId, t, k).
+ * waitRecvCostStats (diagnose output, may be NULL): [epWorldSize] int32, per
+ * source rank the microseconds the dispatch spent on that rank's rows,
+ * accumulated across calls (moe_dispatch_normal.h:489-529); with one rank,
+ * entry 0 gains the dispatch phase's time on the stream.
  * Limits (moe_dispatch_normal_tiling.cpp:72-94): hidden in [1024,7168] and a
  * multiple of 16 (of 128 for quantMode 3), numTopk in [1,16], moeExpertNum
  * in [1,512], epWorldSize == 1. */
@@ -124,8 +128,8 @@ CAMHIP_API camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(
     const uint16_t *x, const int32_t *topkIdx, const int32_t *sendOffset, const int32_t *sendTokenIdx,
     const int32_t *recvOffset, const int32_t *recvCount, int64_t numTokens, int64_t hidden, int64_t numTopk,
     int64_t epWorldSize, int64_t epRankId, int64_t moeExpertNum, int64_t quantMode, int64_t recvRowsCapacity,
-    void *recvX, float *recvXScales, int32_t *assistInfoForCombine, uint64_t *workspaceSize,
-    camhipExecutor **executor);
+    void *recvX, float *recvXScales, int32_t *assistInfoForCombine, int32_t *waitRecvCostStats,
+    uint64_t *workspaceSize, camhipExecutor **executor);
 CAMHIP_API camhipStatus camhipMoeDispatchNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                 void *stream);
 
@@ -138,12 +142,16 @@ CAMHIP_API camhipStatus camhipMoeDispatchNormal(void *workspace, uint64_t worksp
  * recvTopkWeights [numTokens, numTopk] fp32 -> out [numTokens, hidden] bf16:
  * out[t] = bf16_rne(sum_k float(row(t,k)) * w[t,k]), fp32, k ascending, no FMA.
  * (t,k) slots that received no row contribute nothing.
+ * sendCostStats (diagnose output, may be NULL): [epWorldSize] int32, microseconds
+ * per destination rank, accumulated (moe_combine_normal.h:197); entry 0 gains
+ * the combine phase's time on the stream.
  * Limits: hidden in [1024,7168] and a multiple of 16, numTopk in [1,16],
  * epWorldSize == 1. */
 CAMHIP_API camhipStatus camhipMoeCombineNormalGetWorkspaceSize(
     const uint16_t *recvX, const int32_t *tokenSrcInfo, int64_t numRecvRows, const int32_t *epRecvCounts,
     const float *recvTopkWeights, int64_t numTokens, int64_t numTopk, int64_t hidden, int64_t epWorldSize,
-    int64_t epRankId, int64_t moeExpertNum, uint16_t *out, uint64_t *workspaceSize, camhipExecutor **executor);
+    int64_t epRankId, int64_t moeExpertNum, uint16_t *out, int32_t *sendCostStats, uint64_t *workspaceSize,
+    camhipExecutor **executor);
 CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                void *stream);
 

@@ -77,14 +77,14 @@ def test_layout_workspace_size_and_short_workspace(L):
 
 @pytest.mark.parametrize("H,q,frag", [(1000, 0, "hidden"), (8192, 0, "hidden"), (1040, 3, "128"), (1024, 1, "quantMode")])
 def test_dispatch_rejects_bad_hidden_and_quant(L, H, q, frag):
-    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, H, 2, 1, 0, 8, q, 8, P, P, P)
+    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, H, 2, 1, 0, 8, q, 8, P, P, P, None)
     assert st == 161001 and frag in msg
 
 
 def test_dispatch_and_combine_need_single_rank(L):
-    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, 1024, 2, 2, 0, 8, 0, 8, P, P, P)
+    st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, 1024, 2, 2, 0, 8, 0, 8, P, P, P, None)
     assert st == 161001 and "one EP rank" in msg
-    st, _, _, msg = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 2, 1, 8, P)
+    st, _, _, msg = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 2, 1, 8, P, None)
     assert st == 161001 and "one EP rank" in msg
     st, _, _, msg = _ws(L, "camhipNotifyDispatch", P, 8, 4, 2, 0, P, P, P, P, P, P)
     assert st == 161001 and "one EP rank" in msg
@@ -103,3 +103,17 @@ def test_ops_refuse_cpu_tensors():
     import umdk_amd  # noqa: F401
     with pytest.raises(Exception):
         torch.ops.umdk_cam_op_lib.get_dispatch_layout(torch.zeros(4, 2, dtype=torch.int64), 8, 1)
+
+
+def test_diagnose_outputs_take_workspace(L):
+    # the optional cost-stats outputs add an 8-byte clock stamp to the workspace
+    st, ws0, ex, _ = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, 1024, 2, 1, 0, 8, 0, 8, P, P, P, None)
+    L.camhipReleaseExecutor(ex)
+    st1, ws1, ex, _ = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, 1024, 2, 1, 0, 8, 0, 8, P, P, P, P)
+    L.camhipReleaseExecutor(ex)
+    assert st == 0 and st1 == 0 and ws0 == 0 and ws1 == 8
+    st, wc0, ex, _ = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 1, 0, 8, P, None)
+    L.camhipReleaseExecutor(ex)
+    st1, wc1, ex, _ = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 1, 0, 8, P, P)
+    L.camhipReleaseExecutor(ex)
+    assert st == 0 and st1 == 0 and wc0 == 4 * 4 * 2 and wc1 == wc0 + 8

@@ -214,3 +214,35 @@ def test_error_paths_raise(ops):
                                  0, 1, False)
     with pytest.raises(RuntimeError, match="numTopk"):
         ops.get_dispatch_layout(torch.zeros(4, 17, dtype=torch.int64, device="cuda"), 32, 1)
+
+
+def test_diagnose_cost_stats_accumulate(ops):
+    # the optional waitRecvCostStats / sendCostStats outputs: entry 0 gains each phase's microseconds,
+    # accumulated across calls, and requesting them leaves every other output unchanged
+    from umdk_amd.plan import MoePrefillPlan
+    T, H, E, K = 4096, 7168, 64, 8
+    print(f"diagnose stats T={T} H={H} E={E} K={K}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(T, H, generator=g).bfloat16().cuda()
+    logits = torch.randn(T, E, generator=g).cuda()
+    plan = MoePrefillPlan(T, H, E, K, quant_mode=3, device="cuda")
+    plan.route(logits)
+    plan.layout()
+    plan.dispatch(x)
+    ref_x, ref_idx = plan.expand_x.clone(), plan.expand_idx.clone()
+    y = torch.randn(T * K, H, generator=g).bfloat16().cuda()
+    ref_out = plan.combine(y).clone()
+    ds = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cs = torch.zeros(1, dtype=torch.int32, device="cuda")
+    plan.dispatch(x, cost_stats=ds)
+    out = plan.combine(y, cost_stats=cs)
+    torch.cuda.synchronize()
+    d1, c1 = int(ds.item()), int(cs.item())
+    assert torch.equal(plan.expand_x.view(torch.uint8), ref_x.view(torch.uint8))
+    assert torch.equal(plan.expand_idx, ref_idx) and torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+    # 235 MB written / 470 MB read: tens of microseconds each, and well under a second
+    assert 5 <= d1 < 1_000_000 and 5 <= c1 < 1_000_000, (d1, c1)
+    plan.dispatch(x, cost_stats=ds)
+    plan.combine(y, cost_stats=cs)
+    torch.cuda.synchronize()
+    assert int(ds.item()) >= d1 + 5 and int(cs.item()) >= c1 + 5

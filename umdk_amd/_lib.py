@@ -22,8 +22,8 @@ SIGNATURES = {
     "camhipMoeRoute": "pp iii pp",
     "camhipDispatchLayout": "p iiii pppp",
     "camhipNotifyDispatch": "p iiii pppppp",
-    "camhipMoeDispatchNormal": "pppppp iiiiiiii ppp",
-    "camhipMoeCombineNormal": "pp i pp iiiiii p",
+    "camhipMoeDispatchNormal": "pppppp iiiiiiii pppp",
+    "camhipMoeCombineNormal": "pp i pp iiiiii pp",
     "camhipGroupedMatmulSwiglu": "ppp iiii pp ii pp",
     "camhipGroupedMatmul": "ppp iiii pp i p",
     "camhipFusedDeepMoe": "pppppp p pppp ppp iiiiii iiiii ppp",

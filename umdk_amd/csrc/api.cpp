@@ -229,7 +229,8 @@ camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(const uint16_t *x, const in
                                                      int64_t epWorldSize, int64_t epRankId, int64_t moeExpertNum,
                                                      int64_t quantMode, int64_t recvRowsCapacity, void *recvX,
                                                      float *recvXScales, int32_t *assistInfoForCombine,
-                                                     uint64_t *workspaceSize, camhipExecutor **executor)
+                                                     int32_t *waitRecvCostStats, uint64_t *workspaceSize,
+                                                     camhipExecutor **executor)
 {
     (void)recvOffset;
     (void)recvCount;
@@ -264,11 +265,21 @@ camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(const uint16_t *x, const in
     const int T = (int)numTokens, H = (int)hidden, K = (int)numTopk, E = (int)moeExpertNum, q = (int)quantMode;
     const int rank = (int)epRankId;
     const int cap = recvRowsCapacity > 0x7fffffff ? 0x7fffffff : (int)recvRowsCapacity;
+    // diagnose output: [epWorldSize] int32, microseconds of the dispatch phase per source rank, accumulated
+    int32_t *stats = waitRecvCostStats;
     return make_executor(
-        0,
-        [=](void *, hipStream_t s) {
-            return cam::launch_dispatch(x, topkIdx, sendOffset, sendTokenIdx, T, H, K, E, rank, cap, q, recvX, recvXScales,
-                                        assistInfoForCombine, s);
+        stats ? sizeof(uint64_t) : 0,
+        [=](void *w, hipStream_t s) {
+            if (stats) {
+                hipError_t e = cam::launch_phase_begin((uint64_t *)w, s);
+                if (e != hipSuccess)
+                    return e;
+            }
+            hipError_t e = cam::launch_dispatch(x, topkIdx, sendOffset, sendTokenIdx, T, H, K, E, rank, cap, q, recvX,
+                                                recvXScales, assistInfoForCombine, s);
+            if (e != hipSuccess || !stats)
+                return e;
+            return cam::launch_phase_end((const uint64_t *)w, stats, rank, s);
         },
         workspaceSize, executor);
 }
@@ -283,8 +294,8 @@ camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const
                                                     int64_t numRecvRows, const int32_t *epRecvCounts,
                                                     const float *recvTopkWeights, int64_t numTokens, int64_t numTopk,
                                                     int64_t hidden, int64_t epWorldSize, int64_t epRankId,
-                                                    int64_t moeExpertNum, uint16_t *out, uint64_t *workspaceSize,
-                                                    camhipExecutor **executor)
+                                                    int64_t moeExpertNum, uint16_t *out, int32_t *sendCostStats,
+                                                    uint64_t *workspaceSize, camhipExecutor **executor)
 {
     CHECK_PARAM(epWorldSize == 1 && epRankId == 0,
                 "moe_combine: this build runs one EP rank per GPU (epWorldSize %lld, epRankId %lld; need 1, 0)",
@@ -310,11 +321,24 @@ camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const
     }
     const int N = (int)numRecvRows, T = (int)numTokens, K = (int)numTopk, H = (int)hidden;
     const int32_t *last = epRecvCounts ? epRecvCounts + (moeExpertNum - 1) : nullptr;
-    const uint64_t ws = sizeof(int32_t) * (uint64_t)T * K;
+    // workspace: the row map [T*K] int32, then (diagnose output requested) the phase's start stamp
+    const uint64_t map_bytes = (sizeof(int32_t) * (uint64_t)T * K + 7) & ~(uint64_t)7;
+    int32_t *stats = sendCostStats;
+    const int rank = (int)epRankId;
     return make_executor(
-        ws,
+        map_bytes + (stats ? sizeof(uint64_t) : 0),
         [=](void *w, hipStream_t s) {
-            return cam::launch_combine(recvX, tokenSrcInfo, N, last, recvTopkWeights, T, K, H, out, (int32_t *)w, s);
+            uint64_t *stamp = (uint64_t *)((uint8_t *)w + map_bytes);
+            if (stats) {
+                hipError_t e = cam::launch_phase_begin(stamp, s);
+                if (e != hipSuccess)
+                    return e;
+            }
+            hipError_t e =
+                cam::launch_combine(recvX, tokenSrcInfo, N, last, recvTopkWeights, T, K, H, out, (int32_t *)w, s);
+            if (e != hipSuccess || !stats)
+                return e;
+            return cam::launch_phase_end(stamp, stats, rank, s);
         },
         workspaceSize, executor);
 }

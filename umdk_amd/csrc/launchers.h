@@ -50,6 +50,10 @@ hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, i
                                  const float *topk_w, int T, int K, int H, uint16_t *out, const int32_t *inv,
                                  hipStream_t s);
 
+// ---- diagnose outputs (diag.hip): stats[idx] += microseconds between the two stream points
+hipError_t launch_phase_begin(uint64_t *stamp, hipStream_t s);
+hipError_t launch_phase_end(const uint64_t *stamp, int32_t *stats, int idx, hipStream_t s);
+
 // ---- fused decode helpers (fused.hip)
 hipError_t launch_prepare_ids(const int32_t *ids, const uint8_t *active, int T, int K, int first_local, int L,
                               int32_t *out, hipStream_t s);

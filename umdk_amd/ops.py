@@ -148,7 +148,7 @@ def moe_dispatch_prefill(x, topk_idx, topk_weights, num_tokens_per_expert, send_
     sti = send_token_idx_small if send_token_idx_small.dtype == torch.int32 else send_token_idx_small.to(torch.int32)
     _lib.call("camhipMoeDispatchNormal", _lib.ptr(x), _lib.ptr(ti), _lib.ptr(send_offset), _lib.ptr(sti.contiguous()),
               _lib.ptr(recv_offset), _lib.ptr(recv_count), T, H, K, 1, 0, E, quant_mode, n_rows, _lib.ptr(expand_x),
-              _lib.ptr(scales), _lib.ptr(expand_idx), device=dev)
+              _lib.ptr(scales), _lib.ptr(expand_idx), None, device=dev)
     return expand_x, scales, expand_idx, recv_count, rtpe
 
 
@@ -172,7 +172,7 @@ def moe_combine_prefill(x, topk_idx, topk_weights, src_idx, send_head, group_ep,
     out = torch.empty((T, H), dtype=x.dtype, device=x.device)
     sh = send_head if send_head.dtype == torch.int32 else send_head.to(torch.int32)
     _lib.call("camhipMoeCombineNormal", _lib.ptr(x), _lib.ptr(src_idx.contiguous()), N, _lib.ptr(sh.contiguous()),
-              _lib.ptr(w), T, K, H, 1, 0, E, _lib.ptr(out), device=x.device)
+              _lib.ptr(w), T, K, H, 1, 0, E, _lib.ptr(out), None, device=x.device)
     return out
 
 

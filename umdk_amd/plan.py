@@ -39,9 +39,13 @@ class MoePrefillPlan:
         self.expand_idx = torch.empty(N * 3, **i32)
         self.out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
         ws_layout = _lib.workspace_size("camhipDispatchLayout", 1, T, 1, E, K, None, 1, None, 1)
-        ws_combine = _lib.workspace_size("camhipMoeCombineNormal", 1, 1, N, None, 1, T, K, H, 1, 0, E, 1)
+        # sized with the diagnose output requested (the larger workspace), so either call fits
+        ws_combine = _lib.workspace_size("camhipMoeCombineNormal", 1, 1, N, None, 1, T, K, H, 1, 0, E, 1, 1)
+        ws_dispatch = _lib.workspace_size("camhipMoeDispatchNormal", 1, 1, 1, 1, None, None, T, H, K, 1, 0, E,
+                                          quant_mode, N, 1, 1, 1, 1)
         self.ws_layout = torch.empty(max(ws_layout, 1), dtype=torch.uint8, device=dev)
         self.ws_combine = torch.empty(max(ws_combine, 1), dtype=torch.uint8, device=dev)
+        self.ws_dispatch = torch.empty(max(ws_dispatch, 1), dtype=torch.uint8, device=dev)
 
     # -- stages ---------------------------------------------------------
     def route(self, logits, bias=None, stream=None):
@@ -58,17 +62,22 @@ class MoePrefillPlan:
                     self.recv_offset.data_ptr(), self.max_bs.data_ptr(), self.recv_tokens_per_expert.data_ptr(),
                     stream=stream, device=self.device)
 
-    def dispatch(self, x, stream=None):
+    def dispatch(self, x, stream=None, cost_stats=None):
+        """cost_stats: optional [1] int32 device tensor; gains the dispatch phase's microseconds
+        (the reference's waitRecvCostStats diagnose output)."""
         _lib.launch("camhipMoeDispatchNormal", x.data_ptr(), self.topk_idx.data_ptr(), self.send_offset.data_ptr(),
                     self.send_token_idx.data_ptr(), self.recv_offset.data_ptr(), self.recv_count.data_ptr(), self.T,
                     self.H, self.K, 1, 0, self.E, self.q, self.N, self.expand_x.data_ptr(), self.scales.data_ptr(),
-                    self.expand_idx.data_ptr(), stream=stream, device=self.device)
+                    self.expand_idx.data_ptr(), None if cost_stats is None else cost_stats.data_ptr(),
+                    workspace=self.ws_dispatch, stream=stream, device=self.device)
 
-    def combine(self, y, stream=None):
-        """y: [N, H] bf16 expert outputs in dispatch order."""
+    def combine(self, y, stream=None, cost_stats=None):
+        """y: [N, H] bf16 expert outputs in dispatch order.  cost_stats: optional [1] int32 device
+        tensor; gains the combine phase's microseconds (the reference's sendCostStats)."""
         _lib.launch("camhipMoeCombineNormal", y.data_ptr(), self.expand_idx.data_ptr(), self.N,
                     self.recv_count.data_ptr(), self.topk_w.data_ptr(), self.T, self.K, self.H, 1, 0, self.E,
-                    self.out.data_ptr(), workspace=self.ws_combine, stream=stream, device=self.device)
+                    self.out.data_ptr(), None if cost_stats is None else cost_stats.data_ptr(),
+                    workspace=self.ws_combine, stream=stream, device=self.device)
         return self.out
 
 
