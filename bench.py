@@ -1,6 +1,6 @@
 """Benchmark of the CAM MoE hot path on one MI355X.
 
-Default workload ("dispatch/combine at the DeepSeek-V3
+Default workload (benchmark config 2, "dispatch/combine at the DeepSeek-V3
 one-rank shape"): T=4096 tokens, H=7168, E=256 experts, top-8, router logits
 ~N(0,1) plus a per-expert bias ~N(0,0.5); one step = route -> layout -> count
 exchange -> fp8 1x128 dispatch -> combine of identity-expert bf16 rows.

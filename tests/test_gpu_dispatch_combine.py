@@ -174,7 +174,7 @@ def test_combine_matches_oracle_bit_exact(ops, seed, T, H, E, K):
 
 
 def test_cfg1_identity_experts_closed_form(ops):
-    # BASELINE config 1 / test_moe_dispatch_combine_prefill.py:163-168: with
+    # benchmark config 1 / test_moe_dispatch_combine_prefill.py:163-168: with
     # identity experts, combine(dispatch(x)) = x * sum_k w_k
     T, H, E, K = 128, 1024, 8, 2
     x, logits, _ = make_inputs(0, T, H, E, K)

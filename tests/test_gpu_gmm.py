@@ -2,7 +2,7 @@
 the CPU oracle at small ragged shapes and against a torch fp32 reference on
 the GPU at larger shapes.
 
-Tolerances: bf16 within 2e-2 relative, fp8 within 5e-2
+Tolerances (the project target): bf16 within 2e-2 relative, fp8 within 5e-2
 relative, measured as max|got - ref| / max|ref| per output tensor.  The
 reference's own fused-vs-small-op check is allclose(rtol=0.02, atol=2.0) on a
 fraction of elements (test_fused_deep_moe.py:443, util/tool.py:47-65); the
