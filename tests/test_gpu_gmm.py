@@ -212,3 +212,9 @@ def test_gmm_short_segments_in_large_capacity_take_128_row_tile(ops, dtype):
 def test_gmm_fp8_long_reduction(ops):
     # k = 17408 (136 k-steps, past any per-tile staging of the weight scales)
     _ragged_vs_torch(ops, [40, 3], 17408, 128, "fp8", 0, 24)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_mixed_tile_heights_in_one_launch(ops, dtype):
+    # experts with >= 384 rows take 256-row tiles, the others 128-row tiles, in the same launch
+    _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383], 1024, 256, dtype, 7, 25)

@@ -83,9 +83,12 @@ struct GroupTable {
     int row_off[G_MAX_L + 1];      // exclusive prefix of rows per expert
 };
 
-// Block-wide exclusive scans of ceil(cnt/GBM) and cnt over the L experts.
+// Block-wide exclusive scans of the M-tiles and rows per expert.  Only experts with a row count in
+// [lo, hi) get tiles (a launch may split the experts between two tile heights); the row offsets
+// count every expert (they locate segments in dispatch order).
 template <int GBM, int GTHREADS>
-__device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch)
+__device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch, int lo,
+                                  int hi)
 {
     const int tid = threadIdx.x;
     const int per = (L + GTHREADS - 1) / GTHREADS;
@@ -94,7 +97,7 @@ __device__ void build_group_table(const int64_t *__restrict__ group_list, int L,
         const int e = tid * per + q;
         if (e < L) {
             const int c = (int)group_list[e];
-            tsum += (c + GBM - 1) / GBM;
+            tsum += (c >= lo && c < hi) ? (c + GBM - 1) / GBM : 0;
             rsum += c;
         }
     }
@@ -121,7 +124,7 @@ __device__ void build_group_table(const int64_t *__restrict__ group_list, int L,
             const int c = (int)group_list[e];
             gt.tile_prefix[e] = ta;
             gt.row_off[e] = ra;
-            ta += (c + GBM - 1) / GBM;
+            ta += (c >= lo && c < hi) ? (c + GBM - 1) / GBM : 0;
             ra += c;
         }
     }
@@ -178,7 +181,8 @@ __device__ __forceinline__ void lds_sync()
     bar();
 }
 
-template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p)
+// Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
+template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first)
 {
     using TC = Tile<BM>;
     constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
@@ -189,7 +193,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
     int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GMAX_THREADS ints: table scan, then the fp8 amax exchange
 
-    build_group_table<GBM, GTHREADS>(p.group_list, p.L, *gt, scratch);
+    build_group_table<GBM, GTHREADS>(p.group_list, p.L, *gt, scratch, lo, hi);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -206,9 +210,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     const int ntn = SWIGLU ? half_n / 128 : p.N / GBN;
     const int total = __builtin_amdgcn_readfirstlane(gt->tile_prefix[p.L]) * ntn;
 
-    // XCD-aware order: blocks b, b+8, b+16, ... run on the same XCD; give them consecutive tiles
     const int G = gridDim.x;
-    const int logical = (G & 7) ? (int)blockIdx.x : (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
+    const int logical = first;
 
     // DMA slot of this lane inside a 1 KiB band (8 rows x 128 B): row l/8, physical chunk l%8,
     // which holds logical chunk (l%8) ^ ((row >> 1) & 7) -- see swz()
@@ -768,40 +771,63 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     }
 }
 
+// XCD-aware order: blocks b, b+8, b+16, ... run on the same XCD; give them consecutive positions,
+// so that a run of consecutive tiles shares that XCD's L2
+__device__ __forceinline__ int xcd_position()
+{
+    const int G = gridDim.x;
+    return (G & 7) ? (int)blockIdx.x : (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
+}
+
 // Decode-sized segments: the 32-row tile (4 waves).
 template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_small(GmmArgs p)
 {
-    gmm_body<DT, EPI, 32>(p);
+    gmm_body<DT, EPI, 32>(p, 0, 0x7fffffff, xcd_position());
 }
 
 // Prefill: 8 waves, 128- or 256-row tile picked per launch from the actual rows per touched
 // expert (counts are on the device).  The choice is block-uniform and identical in every block.
+// Experts with at least this many rows take the 256-row tile (when the launch allows it).
+constexpr int G_HEAVY_ROWS = 384;
+
+// Prefill: 8 waves.  With the 256-row tile allowed, the experts holding at least G_HEAVY_ROWS rows run
+// 256-row tiles first, then the rest 128-row tiles -- one launch, the longest tiles first, the tile
+// sequence of each block continuing round-robin from the first class into the second.  A layer whose
+// load is skewed (a few experts with a thousand rows, many with a handful) gets tall tiles where they
+// halve the operand traffic and short ones where a tall tile would multiply padding.
 template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
 {
-    // the first bytes of the dynamic LDS serve as the reduction slots before the tile body starts
+    // the first bytes of the dynamic LDS serve as the reduction slot before the tile body starts
     // (a static __shared__ array would push the 1 KiB-aligned dynamic region past the LDS limit)
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int pos = xcd_position();
+    // short reductions keep the 128-row tile: the 256-row tile's per-tile ring fill and drain would
+    // not amortise over fewer than 32 k-steps
+    const int nk = (int)((uint32_t)p.K * (DT == DT_BF16 ? 2 : 1) / GKB);
+    if (!p.allow256 || nk < 32) {
+        gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, pos);
+        return;
+    }
     int *red = reinterpret_cast<int *>(smem);
-    if (threadIdx.x < 2)
-        red[threadIdx.x] = 0;
+    if (threadIdx.x == 0)
+        red[0] = 0;
     __syncthreads();
-    int rows = 0, touched = 0;
+    int heavy = 0;  // 256-row tiles of the heavy experts
     for (int e = threadIdx.x; e < p.L; e += blockDim.x) {
         const int c = (int)p.group_list[e];
-        rows += c;
-        touched += c > 0;
+        heavy += c >= G_HEAVY_ROWS ? (c + 255) / 256 : 0;
     }
-    if (rows)
-        atomicAdd(&red[0], rows);
-    if (touched)
-        atomicAdd(&red[1], touched);
+    if (heavy)
+        atomicAdd(&red[0], heavy);
     __syncthreads();
-    const int r = red[0] / (red[1] > 0 ? red[1] : 1);
+    const int n_heavy = red[0];
     __syncthreads();
-    if (p.allow256 && r >= 512)
-        gmm_body<DT, EPI, 256>(p);
-    else
-        gmm_body<DT, EPI, 128>(p);
+    const int G = gridDim.x;
+    if (n_heavy > 0) {
+        gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
+        __syncthreads();  // every wave is done with the first class's ring and table
+    }
+    gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, ((pos - n_heavy) % G + G) % G);
 }
 
 template <int BM> constexpr size_t lds_bytes()
@@ -852,7 +878,7 @@ template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s
         hipLaunchKernelGGL((gmm_kernel_small<DT, EPI>), dim3(grid), dim3(256), lds, s, a);
         return hipGetLastError();
     }
-    a.allow256 = a.M >= 512 * a.L;
+    a.allow256 = a.M >= G_HEAVY_ROWS;  // some expert may reach the 256-row tile class
     static bool done = false;
     const size_t lds = lds_bytes<128>() > lds_bytes<256>() ? lds_bytes<128>() : lds_bytes<256>();
     hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, done);
