@@ -241,7 +241,7 @@ def run_decode(steps, seed, dtype="fp8"):
 
     def step():
         # routing over all 256 experts; ids of the 224 non-local experts are not routed on this rank
-        _lib.launch("camhipMoeRoute", logits.data_ptr(), None, T, E, K, ids.data_ptr(), wts.data_ptr(),
+        _lib.launch("camhipMoeRoute", logits.data_ptr(), None, T, E, K, ids.data_ptr(), wts.data_ptr(), None,
                     device=dev)
         _lib.launch("camhipFusedDeepMoe", *fargs, workspace=ws, device=dev)
 

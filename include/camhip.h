@@ -62,11 +62,13 @@ CAMHIP_API void camhipReleaseExecutor(camhipExecutor *executor);
  * logits [numTokens, numExperts] fp32, bias [numExperts] fp32 or NULL.
  * topkIdx[t,k]: the k-th largest logit+bias (ties -> lower expert id).
  * topkWeights[t,k] = softmax(logits[t])[topkIdx[t,k]] renormalised over the K picks.
+ * topkIdxInt64 (optional, may be NULL): the same ids as int64, the input type of
+ * camhipDispatchLayout (aclnnDispatchLayout takes int64 topk_idx).
  * Limits: 1 <= topK <= 16, topK <= numExperts <= 512. */
 CAMHIP_API camhipStatus camhipMoeRouteGetWorkspaceSize(const float *logits, const float *bias, int64_t numTokens,
                                                        int64_t numExperts, int64_t topK, int32_t *topkIdx,
-                                                       float *topkWeights, uint64_t *workspaceSize,
-                                                       camhipExecutor **executor);
+                                                       float *topkWeights, int64_t *topkIdxInt64,
+                                                       uint64_t *workspaceSize, camhipExecutor **executor);
 CAMHIP_API camhipStatus camhipMoeRoute(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                        void *stream);
 

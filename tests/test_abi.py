@@ -91,9 +91,9 @@ def test_dispatch_and_combine_need_single_rank(L):
 
 
 def test_route_limits(L):
-    st, _, _, msg = _ws(L, "camhipMoeRoute", P, None, 4, 8, 9, P, P)
+    st, _, _, msg = _ws(L, "camhipMoeRoute", P, None, 4, 8, 9, P, P, None)
     assert st == 161001 and "topK" in msg
-    st, ws, ex, _ = _ws(L, "camhipMoeRoute", P, None, 4, 8, 2, P, P)
+    st, ws, ex, _ = _ws(L, "camhipMoeRoute", P, None, 4, 8, 2, P, P, None)
     assert st == 0 and ws == 0
     assert L.camhipMoeRoute(None, 0, None, None) == 161002  # NULL executor
 

@@ -246,3 +246,19 @@ def test_diagnose_cost_stats_accumulate(ops):
     plan.combine(y, cost_stats=cs)
     torch.cuda.synchronize()
     assert int(ds.item()) >= d1 + 5 and int(cs.item()) >= c1 + 5
+
+
+def test_route_int64_copy_of_ids(ops):
+    # the optional int64 output of the route op carries the same ids (the layout op's input type)
+    from umdk_amd.plan import MoePrefillPlan
+    T, H, E, K = 1000, 1024, 256, 8
+    print(f"route int64 ids T={T} E={E} K={K}", flush=True)
+    g = torch.Generator().manual_seed(4)
+    logits = torch.randn(T, E, generator=g).cuda()
+    bias = (torch.randn(E, generator=g) * 0.5).cuda()
+    plan = MoePrefillPlan(T, H, E, K, quant_mode=0, device="cuda")
+    plan.route(logits, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.topk_idx64, plan.topk_idx.long())
+    ref_idx, _ = orc.route(logits.cpu().numpy(), bias.cpu().numpy(), K)
+    assert np.array_equal(plan.topk_idx.cpu().numpy(), ref_idx)

@@ -19,7 +19,7 @@ _EXP = ctypes.POINTER(ctypes.c_void_p)
 
 # argument kinds of each *GetWorkspaceSize entry point ('p' pointer, 'i' int64)
 SIGNATURES = {
-    "camhipMoeRoute": "pp iii pp",
+    "camhipMoeRoute": "pp iii ppp",
     "camhipDispatchLayout": "p iiii pppp",
     "camhipNotifyDispatch": "p iiii pppppp",
     "camhipMoeDispatchNormal": "pppppp iiiiiiii pppp",

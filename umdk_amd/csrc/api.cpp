@@ -127,7 +127,8 @@ void camhipReleaseExecutor(camhipExecutor *executor) { delete executor; }
 // ---------------------------------------------------------------- routing
 camhipStatus camhipMoeRouteGetWorkspaceSize(const float *logits, const float *bias, int64_t numTokens,
                                             int64_t numExperts, int64_t topK, int32_t *topkIdx, float *topkWeights,
-                                            uint64_t *workspaceSize, camhipExecutor **executor)
+                                            int64_t *topkIdxInt64, uint64_t *workspaceSize,
+                                            camhipExecutor **executor)
 {
     CHECK_PARAM(numTokens >= 0 && numTokens <= kMaxTokens, "moe_route: numTokens %lld out of [0,%lld]",
                 (long long)numTokens, (long long)kMaxTokens);
@@ -142,7 +143,10 @@ camhipStatus camhipMoeRouteGetWorkspaceSize(const float *logits, const float *bi
     }
     const int T = (int)numTokens, E = (int)numExperts, K = (int)topK;
     return make_executor(
-        0, [=](void *, hipStream_t s) { return cam::launch_route(logits, bias, T, E, K, topkIdx, topkWeights, s); },
+        0,
+        [=](void *, hipStream_t s) {
+            return cam::launch_route(logits, bias, T, E, K, topkIdx, topkWeights, s, topkIdxInt64);
+        },
         workspaceSize, executor);
 }
 

@@ -10,8 +10,9 @@ namespace cam {
 enum QuantMode { QUANT_NONE = 0, QUANT_INT8_TOKEN = 2, QUANT_FP8_BLOCK = 3, QUANT_INT8_FUSED = 4 };
 
 // ---- routing (route.hip)
+// topk_idx64 (optional): the same ids as int64, the layout op's input type
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
-                        float *topk_w, hipStream_t s);
+                        float *topk_w, hipStream_t s, int64_t *topk_idx64 = nullptr);
 
 // ---- dispatch layout (layout.hip)
 struct LayoutPlan {

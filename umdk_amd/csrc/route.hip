@@ -53,7 +53,8 @@ template <int PER>
 __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int T, int E,
                                                                  int K, int32_t *__restrict__ topk_idx,
-                                                                 float *__restrict__ topk_w)
+                                                                 float *__restrict__ topk_w,
+                                                                 int64_t *__restrict__ topk_idx64)
 {
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
@@ -116,11 +117,13 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
     if (l16 < K && live) {
         topk_idx[(size_t)t * K + l16] = my_idx;
         topk_w[(size_t)t * K + l16] = my_ex / denom;
+        if (topk_idx64)
+            topk_idx64[(size_t)t * K + l16] = my_idx;
     }
 }
 
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
-                        float *topk_w, hipStream_t s)
+                        float *topk_w, hipStream_t s, int64_t *topk_idx64)
 {
     if (T == 0)
         return hipSuccess;
@@ -131,17 +134,17 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
     const dim3 g(grid), b(ROUTE_WAVES * 64);
     const int per = (E + 15) >> 4;
     if (per <= 1)
-        hipLaunchKernelGGL(route_kernel<1>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<1>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else if (per <= 2)
-        hipLaunchKernelGGL(route_kernel<2>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<2>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else if (per <= 4)
-        hipLaunchKernelGGL(route_kernel<4>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<4>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else if (per <= 8)
-        hipLaunchKernelGGL(route_kernel<8>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<8>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else if (per <= 16)
-        hipLaunchKernelGGL(route_kernel<16>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<16>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else
-        hipLaunchKernelGGL(route_kernel<32>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w);
+        hipLaunchKernelGGL(route_kernel<32>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     return hipGetLastError();
 }
 

@@ -188,7 +188,8 @@ def moe_route(logits, bias, topk):
         b = bias.contiguous()
     idx = torch.empty((T, topk), dtype=torch.int32, device=lg.device)
     w = torch.empty((T, topk), dtype=torch.float32, device=lg.device)
-    _lib.call("camhipMoeRoute", _lib.ptr(lg), _lib.ptr(b), T, E, topk, _lib.ptr(idx), _lib.ptr(w), device=lg.device)
+    _lib.call("camhipMoeRoute", _lib.ptr(lg), _lib.ptr(b), T, E, topk, _lib.ptr(idx), _lib.ptr(w), None,
+              device=lg.device)
     return idx, w
 
 

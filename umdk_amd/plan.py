@@ -49,11 +49,12 @@ class MoePrefillPlan:
 
     # -- stages ---------------------------------------------------------
     def route(self, logits, bias=None, stream=None):
+        # the int64 copy of the ids feeds the layout op (int64 topk_idx, as aclnnDispatchLayout)
         _lib.launch("camhipMoeRoute", logits.data_ptr(), None if bias is None else bias.data_ptr(), self.T, self.E,
-                    self.K, self.topk_idx.data_ptr(), self.topk_w.data_ptr(), stream=stream, device=self.device)
+                    self.K, self.topk_idx.data_ptr(), self.topk_w.data_ptr(), self.topk_idx64.data_ptr(),
+                    stream=stream, device=self.device)
 
     def layout(self, stream=None):
-        self.topk_idx64.copy_(self.topk_idx)
         _lib.launch("camhipDispatchLayout", self.topk_idx64.data_ptr(), self.T, 1, self.E, self.K, None,
                     self.num_tokens_per_expert.data_ptr(), None, self.send_token_idx.data_ptr(),
                     workspace=self.ws_layout, stream=stream, device=self.device)
@@ -111,8 +112,8 @@ class MoeLayerPlan(MoePrefillPlan):
 
     def route(self, logits, bias=None, stream=None):
         _lib.launch("camhipMoeRoute", logits.data_ptr(), None if bias is None else bias.data_ptr(), self.T,
-                    self.E_route, self.K, self.topk_idx.data_ptr(), self.topk_w.data_ptr(), stream=stream,
-                    device=self.device)
+                    self.E_route, self.K, self.topk_idx.data_ptr(), self.topk_w.data_ptr(),
+                    self.topk_idx64.data_ptr(), stream=stream, device=self.device)
 
     def experts(self, w1, w1_scale, w2, w2_scale, stream=None):
         self.gmm1(w1, w1_scale, stream)
