@@ -182,6 +182,7 @@ __device__ __forceinline__ void lds_sync()
 }
 
 // Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
+// (first < 0: balanced placement, see below)
 template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first)
 {
     using TC = Tile<BM>;
@@ -210,8 +211,19 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     const int ntn = SWIGLU ? half_n / 128 : p.N / GBN;
     const int total = __builtin_amdgcn_readfirstlane(gt->tile_prefix[p.L]) * ntn;
 
-    const int G = gridDim.x;
-    const int logical = first;
+    // first < 0: this launch has one tile class, so balance it: with R = ceil(total / grid) rounds, only
+    // the first ceil(total / R) blocks (rounded up to whole XCDs) take tiles, R each at most.  A weight
+    // stream is bound by aggregate HBM bandwidth, which that many CUs still saturate, and no CU is left
+    // streaming a final partial round alone.  Otherwise the caller's position and the full grid stride.
+    int G = gridDim.x, logical = first;
+    if (first < 0) {
+        const int rounds = max((total + G - 1) / G, 1);
+        const int g_eff = min(G, ((total + rounds - 1) / rounds + 7) / 8 * 8);
+        if ((int)blockIdx.x >= g_eff)
+            return;
+        G = g_eff;
+        logical = (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
+    }
 
     // DMA slot of this lane inside a 1 KiB band (8 rows x 128 B): row l/8, physical chunk l%8,
     // which holds logical chunk (l%8) ^ ((row >> 1) & 7) -- see swz()
@@ -782,7 +794,7 @@ __device__ __forceinline__ int xcd_position()
 // Decode-sized segments: the 32-row tile (4 waves).
 template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_small(GmmArgs p)
 {
-    gmm_body<DT, EPI, 32>(p, 0, 0x7fffffff, xcd_position());
+    gmm_body<DT, EPI, 32>(p, 0, 0x7fffffff, -1);
 }
 
 // Prefill: 8 waves, 128- or 256-row tile picked per launch from the actual rows per touched
@@ -805,7 +817,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     // not amortise over fewer than 32 k-steps
     const int nk = (int)((uint32_t)p.K * (DT == DT_BF16 ? 2 : 1) / GKB);
     if (!p.allow256 || nk < 32) {
-        gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, pos);
+        gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, -1);
         return;
     }
     int *red = reinterpret_cast<int *>(smem);
@@ -827,7 +839,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
         __syncthreads();  // every wave is done with the first class's ring and table
     }
-    gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, ((pos - n_heavy) % G + G) % G);
+    gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1);
 }
 
 template <int BM> constexpr size_t lds_bytes()
