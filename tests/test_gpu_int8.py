@@ -250,3 +250,38 @@ def test_int8_rejects_bad_scales(ops):
         ops.grouped_matmul(x, torch.ones(4, device="cuda"), cnt, w, torch.ones(1, 2, 2, device="cuda"))
     with pytest.raises(RuntimeError, match="out_quant=2"):
         ops.grouped_matmul_swiglu(x, torch.ones(4, device="cuda"), cnt, w, torch.ones(1, 256, device="cuda"), 0)
+
+
+@pytest.mark.parametrize("case", [dict(E=16, K=8, bs=16, H=7168, I=2048, eplb=False),    # CASE_4RANK
+                                  dict(E=16, K=8, bs=32, H=7168, I=2048, eplb=True)])    # CASE_8RANK
+def test_fused_int8_reference_cases(ops, case):
+    # the reference test's own recipe on one rank (test_fused_deep_moe.py:276-344, 346-364): round-robin
+    # expert ids arange(bs*K) % E, x ~ U(-5,5) in bf16, int8 weights randint(-16,16) in the logical
+    # [L, H, 2I] / [L, I, H] layouts, fp32 gmm1 scales and bf16 gmm2 scales, per-expert weight lists
+    # when dynamic EPLB is on; counts exact, output within the reference's own bound and 2e-2 max-norm
+    E, K, bs, H, I = case["E"], case["K"], case["bs"], case["H"], case["I"]
+    print(f"fused int8 reference case {case}", flush=True)
+    g = gen(100 + bs)
+    x = (torch.rand(bs, H, generator=g) * 10 - 5).bfloat16()
+    ids = (torch.arange(bs * K, dtype=torch.int32) % E).view(bs, K)
+    scales = torch.rand(bs, K, generator=g)
+    w1 = w_int8(g, (E, H, 2 * I))
+    w2 = w_int8(g, (E, I, H))
+    s1 = ch_scale(g, (E, 2 * I))
+    s2 = ch_scale(g, (E, H)).bfloat16()
+    cx, cids, csc = x.cuda(), ids.cuda(), scales.cuda()
+    if case["eplb"]:
+        g1, g2 = list(w1.cuda().unbind(0)), list(w2.cuda().unbind(0))
+        sc1, sc2 = list(s1.cuda().unbind(0)), list(s2.cuda().unbind(0))
+    else:
+        g1, g2, sc1, sc2 = [w1.cuda()], [w2.cuda()], [s1.cuda()], [s2.cuda()]
+    out, _, etn = ops.fused_deep_moe(cx, cids, g1, sc1, g2, sc2, csc, None, None, None, None, None, None, None,
+                                     "ep", 1, 0, E, 0, 0)
+    d = dict(x=x, ids=ids, scales=scales, w1=w1, w2=w2, s1=s1, s2=s2.float())
+    ref, nte = oracle_moe(d, ids.numpy(), E)
+    assert np.array_equal(etn.cpu().numpy(), nte.astype(np.int64))
+    assert np.array_equal(nte, np.full(E, bs * K // E))          # round robin: every expert gets bs*K/E rows
+    got = out.cpu().float().numpy()
+    refv = orc.bf16_to_f32(ref)
+    assert np.all(np.abs(got - refv) <= 2.0 + 0.02 * np.abs(refv))   # the reference's allclose bound
+    assert relerr(got, refv) < 2e-2
