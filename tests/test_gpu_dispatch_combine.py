@@ -262,3 +262,29 @@ def test_route_int64_copy_of_ids(ops):
     assert torch.equal(plan.topk_idx64, plan.topk_idx.long())
     ref_idx, _ = orc.route(logits.cpu().numpy(), bias.cpu().numpy(), K)
     assert np.array_equal(plan.topk_idx.cpu().numpy(), ref_idx)
+
+
+@pytest.mark.parametrize("use_quant", [False, True])
+def test_reference_prefill_case_identity_experts(ops, use_quant):
+    # test_moe_dispatch_combine_prefill.py:73-175 on one rank: x = c, w = c (c stands for the rank id,
+    # which would be 0 here), topk from argpartition of |randn| + 1, layout -> dispatch -> (int8:
+    # per_token_cast_back) -> combine; out must equal x * sum(w) to calc_diff < 5e-5
+    T, E, K, H, c = 32, 16, 8, 7168, 3.0
+    print(f"reference prefill case use_quant={use_quant}", flush=True)
+    rng = np.random.default_rng(7)
+    x_np = np.full((T, H), c, np.float32)
+    scores = np.abs(rng.standard_normal((T, E)).astype(np.float32)) + 1
+    topk_np = np.argpartition(scores, -K, axis=-1)[:, -K:]
+    w_np = np.full((T, K), c, np.float32)
+    x = torch.from_numpy(x_np).bfloat16().cuda()
+    topk = torch.from_numpy(topk_np.astype(np.int64)).cuda()
+    w = torch.from_numpy(w_np).cuda()
+    nte, sti = ops.get_dispatch_layout(topk, E, 1)
+    recv_x, scales, eidx, rc, _ = ops.moe_dispatch_prefill(x, topk, w, nte, sti, "ep", 0, 1, use_quant)
+    if use_quant:   # per_token_cast_back with one scale per row
+        recv_x = (recv_x.float().view(recv_x.size(0), -1, 128) * scales.view(-1, 1, 1)).view(recv_x.shape).bfloat16()
+    out = ops.moe_combine_prefill(recv_x, topk, w, eidx, rc, "ep", 0, 1)
+    check = out.cpu().float().numpy().astype(np.float64) + 1
+    ref = (x_np * w_np.sum(1, keepdims=True)).astype(np.float64) + 1
+    diff = 1 - 2 * (check * ref).sum() / (check * check + ref * ref).sum()
+    assert diff < 5e-5
