@@ -26,7 +26,6 @@ struct GmmArgs {
     int allow256 = 1;           // set by the launcher: the 256-row tile may be picked on the device
 };
 
-size_t gmm_lds_bytes();
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);
 // Per-token int8 requantisation of the fp32 h written by EPI_SWIGLU_F32AMAX, rows [0, sum(group_list)):
 // q = rint((h * 127) * (1 / amax)), scale = amax * (1/127); rows with amax 0 get q = 0, scale 0.

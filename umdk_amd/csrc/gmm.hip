@@ -849,7 +849,6 @@ template <int BM> constexpr size_t lds_bytes()
 static_assert(lds_bytes<32>() <= 163840 && lds_bytes<128>() <= 163840 && lds_bytes<256>() <= 163840,
               "LDS budget of a gfx950 workgroup");
 
-size_t gmm_lds_bytes() { return lds_bytes<128>() > lds_bytes<32>() ? lds_bytes<128>() : lds_bytes<32>(); }  // upper bound
 
 static int g_num_cus = 0;
 
