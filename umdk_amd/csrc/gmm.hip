@@ -54,11 +54,12 @@ constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
 constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
 
-// Tile shapes.  BM = 128: 2 x 2 waves of 64 x 128, 3-stage ring (prefill: many rows per expert).
-// BM = 32: 1 x 4 waves of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the
-// k-loop is a weight stream and the extra stage keeps more of it in flight).
-// BM = 256 (bf16 only): 8 waves, 2 x 4 of 128 x 64 (two waves per SIMD hide each other's LDS reads),
-// a 2-stage ring -- half the L2->LDS bytes per FLOP of the 128-row tile, for compute-bound prefill.
+// Tile shapes (BM rows x 256 W rows, 128-byte k-steps):
+//   BM = 256: 8 waves, 2 x 4 of 128 x 64, 2-stage ring -- half the L2->LDS bytes per FLOP of the
+//             128-row tile, for compute-bound prefill;
+//   BM = 128: 8 waves, 2 x 4 of 64 x 64, 3-stage ring;
+//   BM = 32:  4 waves, 1 x 4 of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the k-loop
+//             is a weight stream and the extra stage keeps more of it in flight).
 template <int BM_> struct Tile {
     static constexpr int BM = BM_;
     static constexpr int NWAVES = BM >= 128 ? 8 : 4;
