@@ -183,6 +183,45 @@ def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
             "gemm_bound": "mfma" if (f1 + f2) / (peak * 1e12) > (ab1 + ab2) / (HBM_PEAK_GBPS * 1e9) else "hbm"}
 
 
+def measured_peaks():
+    """Practical ceilings of this GPU, for reading the roofline fractions: a STREAM-style device copy and a
+    read-only reduction over 2 GiB (HBM), and the vendor GEMM library on large square-ish GEMMs (MFMA):
+    bf16 through torch.mm, fp8 e4m3 with per-tensor scales through torch._scaled_mm."""
+    dev = torch.device("cuda:0")
+
+    def timed(fn, it=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(it):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / it * 1e-3
+
+    n = 1 << 29  # 2 GiB of fp32
+    src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src))
+    t_sum = timed(lambda: src.sum())
+    del src, dst
+    M = N = K = 8192
+    a16 = torch.randn(M, K, device=dev, dtype=torch.bfloat16)
+    b16 = torch.randn(N, K, device=dev, dtype=torch.bfloat16)
+    t_bf16 = timed(lambda: a16 @ b16.t())
+    a8, b8 = a16.to(torch.float8_e4m3fn), b16.to(torch.float8_e4m3fn)
+    one = torch.tensor(1.0, device=dev)
+    t_fp8 = timed(lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
+    del a16, b16, a8, b8
+    torch.cuda.empty_cache()
+    flop = 2.0 * M * N * K
+    return {"copy_TBps": 2 * 4 * n / t_copy / 1e12, "read_TBps": 4 * n / t_sum / 1e12,
+            "bf16_mm_TFLOPS": flop / t_bf16 / 1e12, "fp8_scaled_mm_TFLOPS": flop / t_fp8 / 1e12,
+            "note": "2 GiB fp32 copy (read + write bytes) and fp32 sum over 2 GiB; 8192^3 GEMMs via the vendor library"}
+
+
 def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536)):
     """fp8 GMM1+GMM2 at DeepSeek-V3 expert shapes (32 experts, H=7168, I=2048) for growing M."""
     from umdk_amd import ops
@@ -285,9 +324,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "5i8", "sweep", "all"],
+    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "5i8", "sweep", "peaks", "all"],
                     help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
-                         "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
+                         "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; peaks: measured copy/read bandwidth and vendor GEMM rates; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
     ap.add_argument("--sweep-m", type=int, default=0, help="--config sweep: only this M")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
@@ -312,6 +351,9 @@ def main():
                                     "bf16", st, wu, args.seed, None)
     cfg4 = lambda st, wu: run_layer("config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), fp8",
                                     4096, 7168, 256, 8, 32, 2048, "fp8", st, wu, args.seed, "zipf")
+    if args.config == "peaks":
+        print(json.dumps({"config": "peaks", "result": measured_peaks()}))
+        return
     if args.config in ("3", "4", "5", "5i8", "sweep"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed),
@@ -404,6 +446,9 @@ def main():
         result["config5"] = run_decode(1000, args.seed)
         torch.cuda.empty_cache()
         result["config5_int8"] = run_decode(1000, args.seed, "int8")
+        torch.cuda.empty_cache()
+    if args.config in ("default", "all"):
+        result["measured_peaks"] = measured_peaks()
         torch.cuda.empty_cache()
     if args.config == "all":
         result["fp8_gemm_sweep"] = gemm_sweep(10, 3, args.seed)
