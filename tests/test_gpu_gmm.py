@@ -218,3 +218,21 @@ def test_gmm_fp8_long_reduction(ops):
 def test_gmm_mixed_tile_heights_in_one_launch(ops, dtype):
     # experts with >= 384 rows take 256-row tiles, the others 128-row tiles, in the same launch
     _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383], 1024, 256, dtype, 7, 25)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_all_groups_empty(ops, dtype):
+    # no rows in any group: every launch shape returns without touching the outputs
+    for cap in (8, 4096):           # the 32-row kernel and the 8-wave kernel
+        print(f"empty groups {dtype} capacity {cap}", flush=True)
+        x = torch.zeros(cap, 1024, device="cuda")
+        w = torch.zeros(3, 512, 1024, device="cuda")
+        gl = torch.zeros(3, dtype=torch.int64, device="cuda")
+        if dtype == "bf16":
+            h, _ = ops.grouped_matmul_swiglu(x.bfloat16(), None, gl, w.bfloat16(), None, 0)
+        else:
+            xq, xs = fp8_quant_rows(x)
+            wq, ws = fp8_quant_weight(w)
+            h, _ = ops.grouped_matmul_swiglu(xq, xs, gl, wq, ws, 3)
+        torch.cuda.synchronize()
+        assert h.shape == (cap, 256)
