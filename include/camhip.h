@@ -173,7 +173,10 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  * logical [L, k, n] layout).  dtype: CAMHIP_DTYPE_BF16, CAMHIP_DTYPE_INT8 or
  * CAMHIP_DTYPE_FP8; for fp8, xScale [m, k/128] and weightScale
  * [numGroups, n/128, k/128] fp32 (dequantised value = code * scale),
- * accumulation fp32; for int8, xScale [m] per token and weightScale
+ * accumulation fp32.  xScaleLayout (fp8 only; 0 for bf16 and int8) says how
+ * xScale is stored: 0 row-major [m, k/128] (as the dispatch writes it; the op
+ * then transposes it into its workspace, m*(k/128)*4 bytes), 1 k-major
+ * [k/128, m] (element (row, b) at b*m + row; read directly, no workspace); for int8, xScale [m] per token and weightScale
  * [numGroups, n] per output channel, exact int32 accumulation and
  * value = ((float)acc * weightScale[n]) * xScale[m]
  * (block_epilogue_per_token_dequant.hpp:338-361). */
@@ -185,18 +188,20 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  * h[m, I] = silu(x W_gate^T) * (x W_up^T), silu(g) = g / (1 + exp(-g))
  * (block_epilogue_per_token_dequant_swiglu.h:256-286).
  * outQuant CAMHIP_QUANT_NONE: h bf16; CAMHIP_QUANT_FP8_BLOCK: h fp8 e4m3fn with
- * hScale [m, I/128], quantised per 1x128 block like the dispatch quantiser.
+ * hScale stored k-major [I/128, m] (ready for GMM2 with xScaleLayout 1),
+ * quantised per 1x128 block like the dispatch quantiser.
  * int8 inputs require outQuant CAMHIP_QUANT_INT8_TOKEN: h int8 [m, I] with
  * hScale [m], requantised per token over the whole row,
  * q = rint((h * 127) * (1/amax)), scale = amax * (1/127)
  * (post_swiglu_dynamic_quant.h:164-231); this mode needs a workspace of
- * m*I*4 + m*4 bytes (fp32 h and the row maxima), the others none.
+ * m*I*4 + m*4 bytes (fp32 h and the row maxima); fp8 with row-major xScale
+ * needs the transposed scales' workspace; the others none.
  * Limits: 1 <= numGroups <= 512, k a multiple of 64 (bf16) / 128 (fp8, int8),
  * I a multiple of 128, m*k and n*k bytes below 4 GiB. */
 CAMHIP_API camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(
     const void *x, const float *xScale, const int64_t *groupList, int64_t numGroups, int64_t m, int64_t k, int64_t n,
-    const void *weight, const float *weightScale, int64_t dtype, int64_t outQuant, void *h, float *hScale,
-    uint64_t *workspaceSize, camhipExecutor **executor);
+    const void *weight, const float *weightScale, int64_t dtype, int64_t xScaleLayout, int64_t outQuant, void *h,
+    float *hScale, uint64_t *workspaceSize, camhipExecutor **executor);
 CAMHIP_API camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                   void *stream);
 
@@ -205,7 +210,8 @@ CAMHIP_API camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t work
 CAMHIP_API camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const float *xScale,
                                                             const int64_t *groupList, int64_t numGroups, int64_t m,
                                                             int64_t k, int64_t n, const void *weight,
-                                                            const float *weightScale, int64_t dtype, uint16_t *out,
+                                                            const float *weightScale, int64_t dtype,
+                                                            int64_t xScaleLayout, uint16_t *out,
                                                             uint64_t *workspaceSize, camhipExecutor **executor);
 CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                             void *stream);

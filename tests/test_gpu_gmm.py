@@ -53,7 +53,7 @@ def fp8_quant_weight(w):
 
 def dq_rows(q, s):
     m, k = q.shape
-    return (q.float().view(m, k // 128, 128) * s.float().view(m, k // 128, 1)).view(m, k)
+    return (q.float().view(m, k // 128, 128) * s.float().reshape(m, k // 128, 1)).view(m, k)
 
 
 # the first two cases take the 32-row tile (rows <= 48 per expert), the others the 128-row tile
@@ -236,3 +236,28 @@ def test_gmm_all_groups_empty(ops, dtype):
             h, _ = ops.grouped_matmul_swiglu(xq, xs, gl, wq, ws, 3)
         torch.cuda.synchronize()
         assert h.shape == (cap, 256)
+
+
+def test_gmm_fp8_scale_layouts_agree(ops):
+    # row-major x_scale (transposed by the op into its workspace) and k-major x_scale (read directly)
+    # give bit-identical results; rows past the group sum and an empty group included
+    print("gmm fp8 scale layouts", flush=True)
+    counts = [130, 0, 257, 64]
+    H, I = 1024, 256
+    g = torch.Generator(device="cuda").manual_seed(11)
+    M = sum(counts) + 5
+    xq, xs = fp8_quant_rows(torch.randn(M, H, device="cuda", generator=g))
+    w1q, w1s = fp8_quant_weight(torch.randn(4, 2 * I, H, device="cuda", generator=g) * 0.05)
+    w2q, w2s = fp8_quant_weight(torch.randn(4, H, I, device="cuda", generator=g) * 0.05)
+    gl = torch.tensor(counts, dtype=torch.int64, device="cuda")
+    xs_k = xs.t().contiguous().t()
+    assert not xs_k.is_contiguous()
+    h0, hs0 = ops.grouped_matmul_swiglu(xq, xs.contiguous(), gl, w1q, w1s, 3)
+    h1, hs1 = ops.grouped_matmul_swiglu(xq, xs_k, gl, w1q, w1s, 3)
+    n = sum(counts)
+    assert torch.equal(h0[:n].view(torch.uint8), h1[:n].view(torch.uint8))
+    assert torch.equal(hs0[:n], hs1[:n])
+    assert tuple(hs0.shape) == (M, I // 128) and hs0.t().is_contiguous()
+    o0 = ops.grouped_matmul(h0, hs0, gl, w2q, w2s)                     # k-major h scales
+    o1 = ops.grouped_matmul(h0, hs0.contiguous(), gl, w2q, w2s)        # same values, row-major
+    assert torch.equal(o0[:n], o1[:n])

@@ -24,8 +24,8 @@ SIGNATURES = {
     "camhipNotifyDispatch": "p iiii pppppp",
     "camhipMoeDispatchNormal": "pppppp iiiiiiii pppp",
     "camhipMoeCombineNormal": "pp i pp iiiiii pp",
-    "camhipGroupedMatmulSwiglu": "ppp iiii pp ii pp",
-    "camhipGroupedMatmul": "ppp iiii pp i p",
+    "camhipGroupedMatmulSwiglu": "ppp iiii pp iii pp",
+    "camhipGroupedMatmul": "ppp iiii pp ii p",
     "camhipFusedDeepMoe": "pppppp p pppp ppp iiiiii iiiii ppp",
 }
 
@@ -64,13 +64,14 @@ def exported_symbols():
         "camhipGetLastErrorMsg", "camhipGetVersion"]
 
 
-def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
+def ptr(t, transposed_ok=False):
+    """Device pointer of a tensor (None -> NULL).  transposed_ok also accepts
+    the transpose of a contiguous 2-D tensor (k-major scale storage)."""
     if t is None:
         return None
     if not t.is_cuda:
         raise CamHipError("umdk_cam_op_lib ops run on the GPU only; got a tensor on " + str(t.device))
-    if not t.is_contiguous():
+    if not (t.is_contiguous() or (transposed_ok and t.dim() == 2 and t.t().is_contiguous())):
         raise CamHipError("umdk_cam_op_lib ops need contiguous tensors")
     return t.data_ptr()
 

@@ -380,10 +380,35 @@ static camhipStatus check_gmm(const char *op, const void *x, const float *xScale
     return CAMHIP_SUCCESS;
 }
 
+// fp8 activation scales reach the kernels k-major ([k/128, m]: one k-step's scales of consecutive rows
+// contiguous); row-major scales ([m, k/128], xScaleLayout 0) are transposed into the workspace first.
+static camhipStatus gmm_executor(const char *op, cam::GmmArgs a, int dt, int epi, int64_t xScaleLayout,
+                                 uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    CHECK_PARAM(xScaleLayout == 0 || xScaleLayout == 1, "%s: xScaleLayout %lld must be 0 (row-major) or 1 (k-major)",
+                op, (long long)xScaleLayout);
+    if (dt != cam::DT_FP8 || xScaleLayout == 1)
+        return make_executor(
+            0, [=](void *, hipStream_t s) { return cam::launch_gmm(a, dt, epi, s); }, workspaceSize, executor);
+    const int nb = a.K / 128;
+    const uint64_t ws = (uint64_t)a.M * nb * sizeof(float);
+    return make_executor(
+        ws,
+        [=](void *w, hipStream_t s) {
+            cam::GmmArgs b = a;
+            hipError_t e = cam::launch_scales_to_kmajor(a.As, a.group_list, a.L, a.M, nb, (float *)w, s);
+            if (e != hipSuccess)
+                return e;
+            b.As = (const float *)w;
+            return cam::launch_gmm(b, dt, epi, s);
+        },
+        workspaceSize, executor);
+}
+
 camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(const void *x, const float *xScale, const int64_t *groupList,
                                                        int64_t numGroups, int64_t m, int64_t k, int64_t n,
                                                        const void *weight, const float *weightScale, int64_t dtype,
-                                                       int64_t outQuant, void *h, float *hScale,
+                                                       int64_t xScaleLayout, int64_t outQuant, void *h, float *hScale,
                                                        uint64_t *workspaceSize, camhipExecutor **executor)
 {
     camhipStatus st = check_gmm("grouped_matmul_swiglu", x, xScale, groupList, numGroups, m, k, n, weight,
@@ -425,8 +450,7 @@ camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(const void *x, const floa
     const int epi = outQuant == CAMHIP_QUANT_FP8_BLOCK ? cam::EPI_SWIGLU_FP8 : cam::EPI_SWIGLU_BF16;
     if (dt == cam::DT_BF16 && epi == cam::EPI_SWIGLU_FP8)
         return fail(CAMHIP_ERROR_INVALID_PARAM, "grouped_matmul_swiglu: fp8 h needs fp8 inputs");
-    return make_executor(
-        0, [=](void *, hipStream_t s) { return cam::launch_gmm(a, dt, epi, s); }, workspaceSize, executor);
+    return gmm_executor("grouped_matmul_swiglu", a, dt, epi, xScaleLayout, workspaceSize, executor);
 }
 
 camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
@@ -437,7 +461,8 @@ camhipStatus camhipGroupedMatmulSwiglu(void *workspace, uint64_t workspaceSize, 
 camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const float *xScale, const int64_t *groupList,
                                                  int64_t numGroups, int64_t m, int64_t k, int64_t n,
                                                  const void *weight, const float *weightScale, int64_t dtype,
-                                                 uint16_t *out, uint64_t *workspaceSize, camhipExecutor **executor)
+                                                 int64_t xScaleLayout, uint16_t *out, uint64_t *workspaceSize,
+                                                 camhipExecutor **executor)
 {
     camhipStatus st = check_gmm("grouped_matmul", x, xScale, groupList, numGroups, m, k, n, weight, weightScale,
                                 dtype, false);
@@ -446,10 +471,7 @@ camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const float *xSc
     CHECK_PTR(out);
     cam::GmmArgs a{(const uint8_t *)x, xScale, groupList, (int)numGroups, (int)m, (int)k, (int)n,
                    (const uint8_t *)weight, weightScale, (uint8_t *)out, nullptr};
-    const int dt = (int)dtype;
-    return make_executor(
-        0, [=](void *, hipStream_t s) { return cam::launch_gmm(a, dt, cam::EPI_PLAIN, s); }, workspaceSize,
-        executor);
+    return gmm_executor("grouped_matmul", a, (int)dtype, cam::EPI_PLAIN, xScaleLayout, workspaceSize, executor);
 }
 
 camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)

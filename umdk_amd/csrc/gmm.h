@@ -13,7 +13,7 @@ enum GmmEpilogue { EPI_PLAIN = 0, EPI_SWIGLU_BF16 = 1, EPI_SWIGLU_FP8 = 2, EPI_S
 
 struct GmmArgs {
     const uint8_t *A;           // [M, K] activations in dispatch order (bf16 or fp8 bytes)
-    const float *As;            // fp8: [M, K/128] activation block scales; int8: [M] per-token scales
+    const float *As;            // fp8: [K/128, M] activation block scales (k-major); int8: [M] per-token scales
     const int64_t *group_list;  // [L] rows per local expert (device)
     int L;                      // local experts
     int M;                      // rows allocated in A and the output
@@ -22,11 +22,15 @@ struct GmmArgs {
     const uint8_t *W;           // [L, N, K]
     const float *Ws;            // fp8: [L, N/128, K/128]; int8: [L, N] per-channel scales
     uint8_t *C;                 // plain: bf16 [M, N]; SwiGLU: h [M, N/2] (bf16, fp8 or fp32)
-    float *Cs;                  // SwiGLU fp8: [M, N/256] h block scales; SwiGLU fp32: [M] row max |h|
+    float *Cs;                  // SwiGLU fp8: [N/256, M] h block scales (k-major); SwiGLU fp32: [M] row max |h|
     int allow256 = 1;           // set by the launcher: the 256-row tile may be picked on the device
 };
 
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);
+// fp8 activation scales [M, nb] row-major -> [nb, M] k-major (the layout the GEMMs read: one k-step's
+// scales of consecutive rows are contiguous), rows [0, sum(group_list)) only.
+hipError_t launch_scales_to_kmajor(const float *src, const int64_t *group_list, int L, int M, int nb, float *dst,
+                                   hipStream_t s);
 // Per-token int8 requantisation of the fp32 h written by EPI_SWIGLU_F32AMAX, rows [0, sum(group_list)):
 // q = rint((h * 127) * (1 / amax)), scale = amax * (1/127); rows with amax 0 get q = 0, scale 0.
 hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64_t *group_list, int L, int M, int I,

@@ -24,7 +24,9 @@
 //     (global_load_lds_dwordx4): no staging registers, and two k-steps of
 //     loads stay in flight while one is multiplied.  Each k-step is 128 bytes
 //     of every A and W row (64 bf16 / 128 fp8 elements); the fp8 activation
-//     scales of the k-step ride the same DMA (4-byte lanes).  A wave's loads
+//     scales of the k-step ride the same DMA (4-byte lanes, read k-major
+//     [K/128, M] so that one k-step's scales of 64 rows are one contiguous
+//     256-byte run; row-major scales are transposed first).  A wave's loads
 //     are counted with s_waitcnt vmcnt and published with a bare s_barrier
 //     (no fence, so outstanding prefetches are not drained).
 //   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row >> 1) & 7:
@@ -290,7 +292,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         // fp8: this wave's activation-scale rows (the WM rows of its row block wm, 64 per DMA)
 #pragma unroll
         for (int d = 0; d < TC::S_DMAS; ++d)
-            c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, p.M - 1) * (uint32_t)nk;
+            c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, p.M - 1);  // k-major: + kc * M
         const int nb = p.N / 128;
         c.wsg = (e * nb + (SWIGLU ? c.n0 : c.n0 + wn * WN) / 128) * nk;
         c.wsu = SWIGLU ? (e * nb + (half_n + c.n0) / 128) * nk : c.wsg;
@@ -306,7 +308,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
         } else {
             const int d = q - A_LOADS - B_LOADS;
-            dma4(p.As + c.gs[d] + kc, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            dma4(p.As + c.gs[d] + (size_t)kc * p.M, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
         }
     };
 
@@ -418,7 +420,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                             *reinterpret_cast<uint32_t *>(hrow + 16 * j) = f32x4_to_e4m3(
                                 h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv, h[i][j][3] * inv);
                         if (wn == 0 && lg == 0)
-                            p.Cs[(size_t)m * (half_n / 128) + n0 / 128] = amax / 448.0f;
+                            p.Cs[(size_t)(n0 / 128) * p.M + m] = amax / 448.0f;  // k-major h scales
                     }
                 }
                 lds_sync();  // red is reused by the next tile
@@ -971,6 +973,55 @@ hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64
         return hipErrorInvalidValue;
     const int grid = M < 4096 ? M : 4096;
     hipLaunchKernelGGL(quant_rows_int8_kernel, dim3(grid), dim3(256), 0, s, h, amax, group_list, L, M, I, q, scale);
+    return hipGetLastError();
+}
+
+// fp8 activation scales row-major [M, nb] -> k-major [nb, M] through an LDS tile: 64 rows x nb per block,
+// read and written in contiguous runs
+__global__ __launch_bounds__(256) void scales_kmajor_kernel(const float *__restrict__ src,
+                                                          const int64_t *__restrict__ group_list, int L, int M,
+                                                          int nb, float *__restrict__ dst)
+{
+    __shared__ float tile[64][129];  // nb <= 128 (k <= 16384 per 64 rows of a pass)
+    __shared__ int tot;
+    if (threadIdx.x == 0)
+        tot = 0;
+    __syncthreads();
+    int part = 0;
+    for (int e = threadIdx.x; e < L; e += blockDim.x)
+        part += (int)group_list[e];
+    if (part)
+        atomicAdd(&tot, part);
+    __syncthreads();
+    const int rows = min(tot, M);
+    for (int r0 = blockIdx.x * 64; r0 < rows; r0 += gridDim.x * 64) {
+        for (int b0 = 0; b0 < nb; b0 += 128) {
+            const int nbc = min(128, nb - b0);
+            for (int i = threadIdx.x; i < 64 * nbc; i += blockDim.x) {
+                const int r = i / nbc, b = i % nbc;
+                tile[r][b] = r0 + r < rows ? src[(size_t)(r0 + r) * nb + b0 + b] : 0.0f;
+            }
+            __syncthreads();
+            for (int i = threadIdx.x; i < 64 * nbc; i += blockDim.x) {
+                const int b = i / 64, r = i % 64;
+                if (r0 + r < rows)
+                    dst[(size_t)(b0 + b) * M + r0 + r] = tile[r][b];
+            }
+            __syncthreads();
+        }
+    }
+}
+
+hipError_t launch_scales_to_kmajor(const float *src, const int64_t *group_list, int L, int M, int nb, float *dst,
+                                   hipStream_t s)
+{
+    if (M < 0 || nb <= 0 || L <= 0)
+        return hipErrorInvalidValue;
+    if (M == 0)
+        return hipSuccess;
+    int blocks = (M + 63) / 64;
+    blocks = blocks < 1024 ? blocks : 1024;
+    hipLaunchKernelGGL(scales_kmajor_kernel, dim3(blocks), dim3(256), 0, s, src, group_list, L, M, nb, dst);
     return hipGetLastError();
 }
 

@@ -217,10 +217,19 @@ def _gmm_common(x, x_scale, group_list, weight, weight_scale, op):
         _check(x_scale is not None and weight_scale is not None, f"{op}: fp8 needs x_scale and weight_scale")
         _check(x_scale.dtype == torch.float32 and tuple(x_scale.shape) == (x.shape[0], k // 128),
                f"{op}: x_scale must be float32 [m, k/128]")
+        _check(x_scale.is_contiguous() or x_scale.t().is_contiguous(),
+               f"{op}: x_scale must be row-major [m, k/128] or the transpose of a contiguous [k/128, m]")
         _check(weight_scale.dtype == torch.float32 and tuple(weight_scale.shape) == (L, n // 128, k // 128),
                f"{op}: weight_scale must be float32 [groups, n/128, k/128]")
         dt = 3
     return dt, L, n, k
+
+
+def _x_scale_layout(x_scale):
+    # 1: fp8 block scales stored k-major ([k/128, m] contiguous, the layout the kernels read); 0: row-major
+    if x_scale is None or x_scale.dim() != 2 or x_scale.is_contiguous():
+        return 0
+    return 1
 
 
 def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quant=0):
@@ -231,7 +240,9 @@ def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quan
     scale for out_quant=0; fp8 h and [m, I/128] scales for out_quant=3; for int8
     x and weights (per-token x_scale [m], per-channel weight_scale [L, 2I]),
     out_quant must be 2: int8 h requantised per token with scales [m]
-    (post_swiglu_dynamic_quant.h:164-231)."""
+    (post_swiglu_dynamic_quant.h:164-231).  fp8 x_scale may be row-major or
+    the transpose of a contiguous [k/128, m]; the fp8 h_scale is returned as
+    such a transpose (k-major storage, which grouped_matmul reads directly)."""
     dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul_swiglu")
     m = x.shape[0]
     I = n // 2
@@ -241,14 +252,14 @@ def grouped_matmul_swiglu(x, x_scale, group_list, weight, weight_scale, out_quan
         hs = torch.empty((m,), dtype=torch.float32, device=x.device)
     elif out_quant == QUANT_FP8_BLOCK:
         h = torch.empty((m, I), dtype=torch.float8_e4m3fn, device=x.device)
-        hs = torch.empty((m, I // 128), dtype=torch.float32, device=x.device)
+        hs = torch.empty((I // 128, m), dtype=torch.float32, device=x.device).t()
     else:
         _check(out_quant == QUANT_NONE, "grouped_matmul_swiglu: out_quant must be 0 or 3")
         h = torch.empty((m, I), dtype=torch.bfloat16, device=x.device)
         hs = torch.empty(0, dtype=torch.float32, device=x.device)
-    _lib.call("camhipGroupedMatmulSwiglu", _lib.ptr(x), _lib.ptr(x_scale), _lib.ptr(group_list), L, m, k, n,
-              _lib.ptr(weight), _lib.ptr(weight_scale), dt, out_quant, _lib.ptr(h),
-              _lib.ptr(hs) if out_quant else None, device=x.device)
+    _lib.call("camhipGroupedMatmulSwiglu", _lib.ptr(x), _lib.ptr(x_scale, True), _lib.ptr(group_list), L, m, k, n,
+              _lib.ptr(weight), _lib.ptr(weight_scale), dt, _x_scale_layout(x_scale), out_quant, _lib.ptr(h),
+              _lib.ptr(hs, True) if out_quant else None, device=x.device)
     return h, hs
 
 
@@ -259,8 +270,9 @@ def grouped_matmul(x, x_scale, group_list, weight, weight_scale):
     dt, L, n, k = _gmm_common(x, x_scale, group_list, weight, weight_scale, "grouped_matmul")
     m = x.shape[0]
     out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
-    _lib.call("camhipGroupedMatmul", _lib.ptr(x), _lib.ptr(x_scale), _lib.ptr(group_list), L, m, k, n,
-              _lib.ptr(weight), _lib.ptr(weight_scale), dt, _lib.ptr(out), device=x.device)
+    _lib.call("camhipGroupedMatmul", _lib.ptr(x), _lib.ptr(x_scale, True), _lib.ptr(group_list), L, m, k, n,
+              _lib.ptr(weight), _lib.ptr(weight_scale), dt, _x_scale_layout(x_scale), _lib.ptr(out),
+              device=x.device)
     return out
 
 
