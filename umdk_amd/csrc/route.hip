@@ -3,9 +3,10 @@
 // Each (score, expert) pair is a 64-bit key: the score's bits mapped to an
 // order-preserving unsigned integer, then ~expert, so the largest key is the
 // largest score with ties going to the lower expert id.  Each of the K
-// rounds takes the row-wide maximum key with four DPP steps (quad xor 1,
-// quad xor 2, half-row mirror, row mirror) -- no LDS traffic -- and the
-// owning lane retires that expert.
+// rounds takes the row-wide maximum of the score part, then of ~expert over
+// the lanes holding that score, each with four DPP max steps (quad xor 1,
+// quad xor 2, half-row mirror, row mirror; no LDS traffic, no branches), and
+// the owning lane retires that expert by zeroing its key.
 // Gates are softmax(logits) at the picks renormalised over the K picks:
 // w_k = exp(l_k - max_l) / sum_j exp(l_j - max_l), summed in pick order.
 // There is no reference routing kernel (callers pass topk_idx; see
@@ -29,13 +30,9 @@ template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v)
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
 
-template <int CTRL> __device__ __forceinline__ void key_max_step(uint32_t &hi, uint32_t &lo)
+template <int CTRL> __device__ __forceinline__ uint32_t umax_step(uint32_t v)
 {
-    const uint32_t ohi = dpp<CTRL>(hi), olo = dpp<CTRL>(lo);
-    if (ohi > hi || (ohi == hi && olo > lo)) {
-        hi = ohi;
-        lo = olo;
-    }
+    return max(v, dpp<CTRL>(v));
 }
 
 template <int CTRL> __device__ __forceinline__ float fmax_step(float v)
@@ -85,26 +82,32 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
     mx = fmax_step<DPP_MIRROR>(mx);
 
     int my_idx = 0;
-    uint32_t taken = 0;  // bit j: slot j already picked (a mask, not a dynamic register index)
 #pragma unroll 1
     for (int k = 0; k < K; ++k) {
-        // lane-local best untaken key (slots ascend in expert id: strict '>' keeps the lower id)
+        // row-wide best score key, then the lowest expert id holding it (picked slots are zeroed):
+        // two branch-free 32-bit max reductions instead of one 64-bit one
         uint32_t hi = 0;
-        int jbest = 0;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const bool gt = !((taken >> j) & 1u) && khi[j] > hi;
-            hi = gt ? khi[j] : hi;
-            jbest = gt ? j : jbest;
-        }
-        uint32_t lo = hi ? ~(uint32_t)(l16 + 16 * jbest) : 0u;
-        key_max_step<DPP_QUAD_XOR1>(hi, lo);
-        key_max_step<DPP_QUAD_XOR2>(hi, lo);
-        key_max_step<DPP_HALF_MIRROR>(hi, lo);
-        key_max_step<DPP_MIRROR>(hi, lo);
+        for (int j = 0; j < PER; ++j)
+            hi = max(hi, khi[j]);
+        hi = umax_step<DPP_QUAD_XOR1>(hi);
+        hi = umax_step<DPP_QUAD_XOR2>(hi);
+        hi = umax_step<DPP_HALF_MIRROR>(hi);
+        hi = umax_step<DPP_MIRROR>(hi);
+        int jb = PER;  // this lane's lowest slot holding the row maximum (slots ascend in expert id)
+#pragma unroll
+        for (int j = PER - 1; j >= 0; --j)
+            jb = khi[j] == hi ? j : jb;
+        uint32_t lo = (hi != 0 && jb < PER) ? ~(uint32_t)(l16 + 16 * jb) : 0u;
+        lo = umax_step<DPP_QUAD_XOR1>(lo);
+        lo = umax_step<DPP_QUAD_XOR2>(lo);
+        lo = umax_step<DPP_HALF_MIRROR>(lo);
+        lo = umax_step<DPP_MIRROR>(lo);
         const int best = (int)~lo;
-        if ((best & 15) == l16)
-            taken |= 1u << (best >> 4);
+        const int clear = (best & 15) == l16 ? best >> 4 : -1;
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            khi[j] = j == clear ? 0u : khi[j];
         if (l16 == k)
             my_idx = best;
     }
