@@ -52,7 +52,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
     const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap, int nchunk,
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
-    int32_t *__restrict__ inv_out)
+    int32_t *__restrict__ inv_out, int kmajor)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
             if (act) {
                 *reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H + col) = q;
                 if ((lane & 7) == 0)
-                    scales[(size_t)row * nb + (col >> 7)] = bscale;
+                    scales[kmajor ? (size_t)(col >> 7) * cap + row : (size_t)row * nb + (col >> 7)] = bscale;
             }
             if (j == 0 && lane == 0 && expand_idx) {
                 expand_idx[(size_t)row * 3 + 0] = rank;
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out,
-                           const float *smooth)
+                           const float *smooth, bool kmajor_scales)
 {
     if (T == 0)
         return hipSuccess;
@@ -266,7 +266,7 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
     switch (quant_mode) {
     case QUANT_NONE:
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_NONE>, grid_chunk, block, 0, s, x, topk_idx, send_offset,
-                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out);
+                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out, 0);
         break;
     case QUANT_INT8_TOKEN:
         hipLaunchKernelGGL(dispatch_int8_kernel<false>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
@@ -282,7 +282,8 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
         if (H & 127)
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_FP8_BLOCK>, grid_chunk, block, 0, s, x, topk_idx,
-                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out);
+                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out,
+                           kmajor_scales ? 1 : 0);
         break;
     default:
         return hipErrorInvalidValue;

@@ -43,8 +43,8 @@ struct Carve {
 };
 
 struct FusedLayout {
-    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, xsk, eidx, h, hs, y, inv, hf, amax;
-    uint64_t sh_x, sh_xs, sh_xsk, sh_h, sh_hs, sh_gl, sh_hf, sh_amax;
+    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv, hf, amax;
+    uint64_t sh_x, sh_xs, sh_h, sh_hs, sh_gl, sh_hf, sh_amax;
     uint64_t bytes;
 };
 
@@ -70,7 +70,6 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool 
     f.sti = c.take(4 * N);
     f.ex = c.take(N * H * esz);
     f.xs = c.take(N * scale_bytes(dt, H));
-    f.xsk = c.take(dt == cam::DT_FP8 ? N * scale_bytes(dt, H) : 0);  // fp8: the same scales k-major for GMM1
     f.eidx = c.take(12 * N);
     f.h = c.take(N * I * esz);
     f.hs = c.take(N * scale_bytes(dt, I));
@@ -81,7 +80,6 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool 
     if (shared) {
         f.sh_x = c.take((uint64_t)T * H * esz);
         f.sh_xs = c.take((uint64_t)T * scale_bytes(dt, H));
-        f.sh_xsk = c.take(dt == cam::DT_FP8 ? (uint64_t)T * scale_bytes(dt, H) : 0);
         f.sh_h = c.take((uint64_t)T * Ish * esz);
         f.sh_hs = c.take((uint64_t)T * scale_bytes(dt, Ish));
         f.sh_gl = c.take(8);
@@ -183,12 +181,7 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
     const int q = dt == cam::DT_FP8 ? cam::QUANT_FP8_BLOCK : int8 ? cam::QUANT_INT8_FUSED : cam::QUANT_NONE;
     const int epi1 = dt == cam::DT_FP8 ? cam::EPI_SWIGLU_FP8 : int8 ? cam::EPI_SWIGLU_F32AMAX : cam::EPI_SWIGLU_BF16;
     // GMM1 + SwiGLU: int8 writes fp32 h and row maxima, then requantises per token
-    // fp8: dispatch writes row-major block scales; GMM1 reads them k-major (kxsk: transposed copy)
-    auto gmm1 = [=](cam::GmmArgs a, float *hf, float *amax, float *xsk, hipStream_t s) -> hipError_t {
-        if (dt == cam::DT_FP8) {
-            HIP_TRY(cam::launch_scales_to_kmajor(a.As, a.group_list, a.L, a.M, a.K / 128, xsk, s));
-            a.As = xsk;
-        }
+    auto gmm1 = [=](cam::GmmArgs a, float *hf, float *amax, hipStream_t s) -> hipError_t {
         if (!int8)
             return cam::launch_gmm(a, dt, epi1, s);
         int8_t *hq = (int8_t *)a.C;
@@ -218,13 +211,14 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             HIP_TRY(cam::launch_notify(counts, L, T, send_off, (int32_t *)P(f.total), recv_cnt, nullptr, nullptr,
                                        expertTokenNums, L, s));
         }
-        // dispatch also writes the combine's row map (inv), so the combine is a single gather
+        // dispatch also writes the combine's row map (inv), so the combine is a single gather; fp8 block
+        // scales come out k-major, the layout GMM1 reads
         HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
                                      (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv),
-                                     expertSmoothScales));
+                                     expertSmoothScales, true));
         cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
                         (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
-        HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), (float *)P(f.xsk), s));
+        HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), s));
         cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
                         (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
         HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
@@ -239,13 +233,13 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             const float *sxs = nullptr;
             if (dt != cam::DT_BF16) {
                 HIP_TRY(cam::launch_dispatch(x, nullptr, nullptr, nullptr, T, H, 1, 1, 0, T, q, P(f.sh_x),
-                                             (float *)P(f.sh_xs), nullptr, s, nullptr, shareSmoothScales));
+                                             (float *)P(f.sh_xs), nullptr, s, nullptr, shareSmoothScales, true));
                 sx = P(f.sh_x);
                 sxs = (const float *)P(f.sh_xs);
             }
             cam::GmmArgs s1{(const uint8_t *)sx, sxs, gl, 1, T, H, 2 * Ish, (const uint8_t *)shareGmm1Weight,
                             shareGmm1WeightScale, (uint8_t *)P(f.sh_h), (float *)P(f.sh_hs)};
-            HIP_TRY(gmm1(s1, (float *)P(f.sh_hf), (float *)P(f.sh_amax), (float *)P(f.sh_xsk), s));
+            HIP_TRY(gmm1(s1, (float *)P(f.sh_hf), (float *)P(f.sh_amax), s));
             cam::GmmArgs s2{(const uint8_t *)P(f.sh_h), (const float *)P(f.sh_hs), gl, 1, T, Ish, H,
                             (const uint8_t *)shareGmm2Weight, shareGmm2WeightScale, (uint8_t *)shareOutput,
                             nullptr};

@@ -978,50 +978,63 @@ hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64
 
 // fp8 activation scales row-major [M, nb] -> k-major [nb, M] through an LDS tile: 64 rows x nb per block,
 // read and written in contiguous runs
+// One block per 64 x 64 tile of (rows, scale blocks): every load of the tile is issued at once (16 per
+// thread, consecutive blocks of a row on consecutive lanes), the tile turns in LDS, and the stores run
+// along the rows.  Rows at or past sum(group_list) are neither read nor written.
 __global__ __launch_bounds__(256) void scales_kmajor_kernel(const float *__restrict__ src,
                                                           const int64_t *__restrict__ group_list, int L, int M,
                                                           int nb, float *__restrict__ dst)
 {
-    __shared__ float tile[64][129];  // nb <= 128 (k <= 16384 per 64 rows of a pass)
+    __shared__ float tile[64][65];
     __shared__ int tot;
-    if (threadIdx.x == 0)
-        tot = 0;
-    __syncthreads();
-    int part = 0;
-    for (int e = threadIdx.x; e < L; e += blockDim.x)
-        part += (int)group_list[e];
-    if (part)
-        atomicAdd(&tot, part);
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        int part = 0;
+#pragma unroll
+        for (int q = 0; q < G_MAX_L / 64; ++q) {
+            const int e = q * 64 + tid;
+            part += e < L ? (int)group_list[e] : 0;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            part += __shfl_xor(part, o, 64);
+        if (tid == 0)
+            tot = part;
+    }
     __syncthreads();
     const int rows = min(tot, M);
-    for (int r0 = blockIdx.x * 64; r0 < rows; r0 += gridDim.x * 64) {
-        for (int b0 = 0; b0 < nb; b0 += 128) {
-            const int nbc = min(128, nb - b0);
-            for (int i = threadIdx.x; i < 64 * nbc; i += blockDim.x) {
-                const int r = i / nbc, b = i % nbc;
-                tile[r][b] = r0 + r < rows ? src[(size_t)(r0 + r) * nb + b0 + b] : 0.0f;
-            }
-            __syncthreads();
-            for (int i = threadIdx.x; i < 64 * nbc; i += blockDim.x) {
-                const int b = i / 64, r = i % 64;
-                if (r0 + r < rows)
-                    dst[(size_t)(b0 + b) * M + r0 + r] = tile[r][b];
-            }
-            __syncthreads();
-        }
+    const int r0 = blockIdx.x * 64, b0 = blockIdx.y * 64;
+    if (r0 >= rows)
+        return;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int idx = i * 256 + tid, r = idx >> 6, b = idx & 63;
+        v[i] = (r0 + r < rows && b0 + b < nb) ? src[(size_t)(r0 + r) * nb + b0 + b] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int idx = i * 256 + tid;
+        tile[idx >> 6][idx & 63] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int idx = i * 256 + tid, b = idx >> 6, r = idx & 63;
+        if (r0 + r < rows && b0 + b < nb)
+            dst[(size_t)(b0 + b) * M + r0 + r] = tile[r][b];
     }
 }
 
 hipError_t launch_scales_to_kmajor(const float *src, const int64_t *group_list, int L, int M, int nb, float *dst,
                                    hipStream_t s)
 {
-    if (M < 0 || nb <= 0 || L <= 0)
+    if (M < 0 || nb <= 0 || L <= 0 || L > G_MAX_L)
         return hipErrorInvalidValue;
     if (M == 0)
         return hipSuccess;
-    int blocks = (M + 63) / 64;
-    blocks = blocks < 1024 ? blocks : 1024;
-    hipLaunchKernelGGL(scales_kmajor_kernel, dim3(blocks), dim3(256), 0, s, src, group_list, L, M, nb, dst);
+    hipLaunchKernelGGL(scales_kmajor_kernel, dim3((M + 63) / 64, (nb + 63) / 64), dim3(256), 0, s, src, group_list, L,
+                       M, nb, dst);
     return hipGetLastError();
 }
 

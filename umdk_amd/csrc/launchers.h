@@ -45,7 +45,8 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
-                           int32_t *inv_out = nullptr, const float *smooth = nullptr);
+                           int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false);
+// (fp8: kmajor_scales writes the block scales as [H/128, cap], the layout the grouped GEMMs read)
 // combine without the scatter launch, for callers whose dispatch already wrote inv
 hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
                                  const float *topk_w, int T, int K, int H, uint16_t *out, const int32_t *inv,
