@@ -76,9 +76,17 @@ def cpu_baseline(T, H, E, K, seed):
         if time.perf_counter() - t0 > 10.0:  # a bounded ~10 s sample of CPU work
             break
     dt = (time.perf_counter() - t0) / reps
-    return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"full config-2 step (T={T}, H={H}, E={E}, K={K}) x{reps} on the C oracle, 1 thread; "
-                      f"{dt * 1e3:.0f} ms/step"}
+    threads = orc.num_threads()
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
+    except OSError:
+        pass
+    return {"value": T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full config-2 step (T={T}, H={H}, E={E}, K={K}) x{reps} on the C oracle, {threads} OpenMP "
+                      f"threads over tokens (route, dispatch, combine; layout serial) of {os.cpu_count()} visible "
+                      f"CPUs ({model}); {dt * 1e3:.0f} ms/step"}
 
 
 BF16_PEAK_TFLOPS = 2500.0

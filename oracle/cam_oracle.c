@@ -43,6 +43,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 #define ORC_API __attribute__((visibility("default")))
 
@@ -110,6 +113,17 @@ ORC_API uint8_t orc_f32_to_e4m3(float x) { return f32_to_e4m3(x); }
 ORC_API float orc_e4m3_to_f32(uint8_t c) { return e4m3_to_f32(c); }
 ORC_API uint16_t orc_f32_to_bf16(float x) { return f32_to_bf16(x); }
 
+/* Threads the token-parallel loops (route, dispatch, combine) use: OpenMP's team size (1 without
+ * OpenMP).  Every token's arithmetic is the same whatever the thread count. */
+ORC_API int orc_num_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
 static inline float silu(float g) { return g / (1.0f + expf(-g)); }
 
 /* ------------------------------------------------------------------ R0 */
@@ -118,7 +132,10 @@ static inline float silu(float g) { return g / (1.0f + expf(-g)); }
 ORC_API void orc_route(const float *logits, const float *bias, int T, int E, int K,
                        int32_t *topk_idx, float *topk_w)
 {
+#pragma omp parallel
+    {
     char *taken = (char *)malloc((size_t)E);
+#pragma omp for schedule(static)
     for (int t = 0; t < T; ++t) {
         const float *l = logits + (size_t)t * E;
         memset(taken, 0, (size_t)E);
@@ -149,6 +166,7 @@ ORC_API void orc_route(const float *logits, const float *bias, int T, int E, int
             topk_w[(size_t)t * K + k] = ex[k] / denom;
     }
     free(taken);
+    }
 }
 
 /* ------------------------------------------------------------------ D1 */
@@ -211,9 +229,12 @@ ORC_API void orc_dispatch(const uint16_t *x, const int32_t *topk_idx, const int3
                           int quant_mode, void *expand_x, float *scales, int32_t *expand_idx)
 {
     int nb = H / 128;
+#pragma omp parallel
+    {
     float *rowf = (float *)malloc(sizeof(float) * (size_t)H);
     uint8_t *q = (uint8_t *)malloc((size_t)H);
     float *bs = (float *)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1));
+#pragma omp for schedule(static)
     for (int t = 0; t < T; ++t) {
         const uint16_t *xr = x + (size_t)t * H;
         for (int h = 0; h < H; ++h)
@@ -261,6 +282,7 @@ ORC_API void orc_dispatch(const uint16_t *x, const int32_t *topk_idx, const int3
     free(rowf);
     free(q);
     free(bs);
+    }
 }
 
 /* Fused-op int8 dispatch (fused_deep_moe/.../cam_moe_distribute_dispatch.h:640-681; the shared
@@ -315,7 +337,10 @@ ORC_API void orc_combine(const uint16_t *y, const int32_t *expand_idx, int N, co
         if (t >= 0 && t < T && k >= 0 && k < K)
             inv[(size_t)t * K + k] = r;
     }
+#pragma omp parallel
+    {
     float *acc = (float *)malloc(sizeof(float) * (size_t)H);
+#pragma omp for schedule(static)
     for (int t = 0; t < T; ++t) {
         for (int h = 0; h < H; ++h)
             acc[h] = 0.0f;
@@ -335,6 +360,7 @@ ORC_API void orc_combine(const uint16_t *y, const int32_t *expand_idx, int N, co
             out[(size_t)t * H + h] = f32_to_bf16(acc[h]);
     }
     free(acc);
+    }
     free(inv);
 }
 

@@ -42,6 +42,11 @@ def _p(a):
     return ctypes.c_void_p(a.ctypes.data) if a is not None else ctypes.c_void_p(0)
 
 
+def num_threads():
+    """Threads of the oracle's token-parallel loops (route, dispatch, combine)."""
+    return int(lib().orc_num_threads())
+
+
 def _c(a, dt):
     return np.ascontiguousarray(a, dtype=dt)
 
