@@ -91,14 +91,16 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
             }
         }
     } else {
-        // lane l quantises columns [1024 j + 16 l, +16): one 16-byte fp8 store per row
+        // lane l quantises columns [1024 j + 16 l, +16): one 16-byte fp8 store per row.  Cached loads of x
+        // and streaming (nontemporal) stores of the rows: measured 5% faster on the DSV3 rank shape than the
+        // reverse (nontemporal loads, cached stores), and 11% faster than cached loads and stores.
         const int col = j * 1024 + lane * 16;
         const bool act = col < H;
         u32x4 raw0 = u32x4{0, 0, 0, 0}, raw1 = u32x4{0, 0, 0, 0};
         if (act) {
             const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col);
-            raw0 = __builtin_nontemporal_load(src);
-            raw1 = __builtin_nontemporal_load(src + 1);
+            raw0 = src[0];
+            raw1 = src[1];
         }
         float f[16];
         unpack_bf16x8(raw0, f);
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
             if (row < 0)
                 continue;
             if (act) {
-                *reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H + col) = q;
+                __builtin_nontemporal_store(q, reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H + col));
                 if ((lane & 7) == 0)
                     scales[kmajor ? (size_t)(col >> 7) * cap + row : (size_t)row * nb + (col >> 7)] = bscale;
             }
