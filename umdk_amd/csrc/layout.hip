@@ -44,13 +44,14 @@ size_t layout_workspace_bytes(int T, int K, int E, int R)
 
 template <typename IdxT>
 __global__ __launch_bounds__(HIST_THREADS) void layout_hist_kernel(const IdxT *__restrict__ topk_idx, int T, int K,
-                                                                   int E, int R, int tpc,
+                                                                   int E, int R, int Rc, int tpc,
                                                                    int32_t *__restrict__ is_token_in_rank,
                                                                    int32_t *__restrict__ counts)
 {
+    // Rc = R when per-rank token counts are requested, else 0 (no rank rows, no per-token rank dedup)
     __shared__ int32_t hist[MAX_E + MAX_R];
     int32_t *rhist = hist + E;
-    for (int i = threadIdx.x; i < E + R; i += HIST_THREADS)
+    for (int i = threadIdx.x; i < E + Rc; i += HIST_THREADS)
         hist[i] = 0;
     __syncthreads();
     const int c = blockIdx.x, nc = gridDim.x;
@@ -62,8 +63,9 @@ __global__ __launch_bounds__(HIST_THREADS) void layout_hist_kernel(const IdxT *_
     if (t < t1) {
         const IdxT *row = topk_idx + (size_t)t * K;
         const int64_t e = row[k];
-        if (e >= 0 && e < E) {
+        if (e >= 0 && e < E)
             atomicAdd(&hist[e], 1);
+        if (Rc > 0 && e >= 0 && e < E) {
             const int r = (int)e / per_rank;
             bool first = true;
             for (int kk = 0; kk < k; ++kk) {
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(HIST_THREADS) void layout_hist_kernel(const IdxT *_
         }
     }
     __syncthreads();
-    for (int q = threadIdx.x; q < E + R; q += HIST_THREADS)
+    for (int q = threadIdx.x; q < E + Rc; q += HIST_THREADS)
         counts[(size_t)q * nc + c] = hist[q];
 }
 
@@ -104,9 +106,21 @@ __global__ __launch_bounds__(256) void layout_scan_kernel(int E, int R, int nc, 
         return;
     int32_t *row = counts + (size_t)q * nc;
     int32_t carry = 0;
+    // the first 256 chunks' counts are loaded before any is scanned (one memory round trip for them)
+    int32_t pre[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        pre[u] = u * 64 + lane < nc ? row[u * 64 + lane] : 0;
     for (int c0 = 0; c0 < nc; c0 += 64) {
         const int c = c0 + lane;
-        const int32_t v = c < nc ? row[c] : 0;
+        int32_t v = 0;
+        if (c0 < 256) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v = c0 == u * 64 ? pre[u] : v;
+        } else {
+            v = c < nc ? row[c] : 0;
+        }
         int32_t incl = v;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -188,12 +202,13 @@ static hipError_t layout_impl(const IdxT *topk_idx, int T, int K, int E, int R, 
         return err;
     }
     int32_t *counts = (int32_t *)ws;
+    const int Rc = ntok_per_rank ? R : 0;
     hipLaunchKernelGGL((layout_hist_kernel<IdxT>), dim3(p.n_chunks), dim3(HIST_THREADS), 0, s, topk_idx, T, K, E, R,
-                       p.tokens_per_chunk, is_token_in_rank, counts);
+                       Rc, p.tokens_per_chunk, is_token_in_rank, counts);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
         return err;
-    hipLaunchKernelGGL(layout_scan_kernel, dim3((E + R + 3) / 4), dim3(256), 0, s, E, R, p.n_chunks, counts,
+    hipLaunchKernelGGL(layout_scan_kernel, dim3((E + Rc + 3) / 4), dim3(256), 0, s, E, Rc, p.n_chunks, counts,
                        ntok_per_expert, ntok_per_rank);
     err = hipGetLastError();
     if (err != hipSuccess)
