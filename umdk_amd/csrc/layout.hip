@@ -149,11 +149,13 @@ __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *_
                                                                    int32_t *__restrict__ send_token_idx)
 {
     __shared__ int32_t wave_hist[RANK_WAVES][MAX_E];
+    __shared__ int32_t base[MAX_E];  // this chunk's exclusive base per expert, loaded beside the ids
     const int c = blockIdx.x, nc = gridDim.x;
     const int w = threadIdx.x >> 6;
+    for (int j = threadIdx.x; j < E; j += RANK_THREADS)
+        base[j] = chunk_base[(size_t)j * nc + c];
     for (int j = threadIdx.x; j < RANK_WAVES * E; j += RANK_THREADS)
         wave_hist[j / E][j % E] = 0;
-    __syncthreads();
     const long i0 = (long)c * tpc * K;
     const long i1 = (long)min(T, (c + 1) * tpc) * K;
     const long i = i0 + threadIdx.x;   // tpc*K <= RANK_THREADS: one entry per thread
@@ -162,6 +164,7 @@ __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *_
         const int64_t v = topk_idx[i];
         e = (v >= 0 && v < E) ? (int)v : -1;
     }
+    __syncthreads();  // wave_hist cleared and base loaded
     const bool valid = e >= 0;
     const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
     uint64_t peers = __ballot(valid);
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *_
     if (i < i1) {
         int32_t rank = -1;
         if (valid) {
-            rank = chunk_base[(size_t)e * nc + c] + inrank;
+            rank = base[e] + inrank;
             for (int ww = 0; ww < w; ++ww)
                 rank += wave_hist[ww][e];
         }
