@@ -117,3 +117,49 @@ def test_diagnose_outputs_take_workspace(L):
     st1, wc1, ex, _ = _ws(L, "camhipMoeCombineNormal", P, P, 8, P, P, 4, 2, 1024, 1, 0, 8, P, P)
     L.camhipReleaseExecutor(ex)
     assert st == 0 and st1 == 0 and wc0 == 4 * 4 * 2 and wc1 == wc0 + 8
+
+
+# grouped GEMMs: "ppp iiii pp iii pp" (SwiGLU) / "ppp iiii pp ii p" (plain)
+def _gmm1(L, m=1024, k=1024, n=512, dt=3, lay=0, oq=3, xs=P, ws=P, groups=4):
+    return _ws(L, "camhipGroupedMatmulSwiglu", P, xs, P, groups, m, k, n, P, ws, dt, lay, oq, P, P)
+
+
+def _gmm2(L, m=1024, k=512, n=1024, dt=3, lay=0, xs=P, ws=P, groups=4):
+    return _ws(L, "camhipGroupedMatmul", P, xs, P, groups, m, k, n, P, ws, dt, lay, P)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(dt=1), "dtype"), (dict(groups=0), "numGroups"), (dict(groups=513), "numGroups"), (dict(m=0), "m "),
+    (dict(k=1000), "multiple"), (dict(n=384), "I a multiple of 128"), (dict(lay=2), "xScaleLayout"),
+    (dict(xs=None), "xScale"), (dict(ws=None), "weightScale"), (dict(dt=2, oq=3), "outQuant 2"),
+    (dict(dt=0, oq=3), "fp8 h needs fp8 inputs"),
+])
+def test_gmm1_rejects_bad_arguments(L, kw, frag):
+    st, _, ex, msg = _gmm1(L, **kw)
+    assert st != 0 and frag in msg, msg
+
+
+@pytest.mark.parametrize("kw,frag", [(dict(n=640), "multiple of 256"), (dict(k=96, dt=0), "multiple of 64"),
+                                     (dict(lay=-1), "xScaleLayout")])
+def test_gmm2_rejects_bad_arguments(L, kw, frag):
+    st, _, ex, msg = _gmm2(L, **kw)
+    assert st != 0 and frag in msg, msg
+
+
+def test_gmm_workspace_sizes(L):
+    # fp8 with row-major activation scales: their k-major copy, m * (k/128) floats
+    st, ws, ex, _ = _gmm1(L, m=1024, k=1024, lay=0)
+    L.camhipReleaseExecutor(ex)
+    assert st == 0 and ws == 1024 * 8 * 4
+    # k-major scales (as GMM1 writes h_scale for GMM2) and bf16 need none
+    for args in (dict(lay=1), dict(dt=0, oq=0, xs=None, ws=None)):
+        st, ws, ex, _ = _gmm1(L, **args)
+        L.camhipReleaseExecutor(ex)
+        assert st == 0 and ws == 0, args
+    st, ws, ex, _ = _gmm2(L, lay=1)
+    L.camhipReleaseExecutor(ex)
+    assert st == 0 and ws == 0
+    # int8 SwiGLU: fp32 h and the row maxima before the per-token requantisation
+    st, ws, ex, _ = _gmm1(L, m=1000, k=1024, n=512, dt=2, oq=2)
+    L.camhipReleaseExecutor(ex)
+    assert st == 0 and ws >= 1000 * 256 * 4 + 1000 * 4
