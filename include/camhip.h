@@ -194,7 +194,7 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  * hScale [m], requantised per token over the whole row,
  * q = rint((h * 127) * (1/amax)), scale = amax * (1/127)
  * (post_swiglu_dynamic_quant.h:164-231); this mode needs a workspace of
- * m*I*4 + m*4 bytes (fp32 h and the row maxima); fp8 with row-major xScale
+ * m*I*4 + m*(I/32)*4 bytes (fp32 h and its partial row maxima); fp8 with row-major xScale
  * needs the transposed scales' workspace; the others none.
  * Limits: 1 <= numGroups <= 512, k a multiple of 64 (bf16) / 128 (fp8, int8),
  * I a multiple of 128, m*k and n*k bytes below 4 GiB. */

@@ -417,12 +417,13 @@ camhipStatus camhipGroupedMatmulSwigluGetWorkspaceSize(const void *x, const floa
         return st;
     CHECK_PTR(h);
     if (dtype == CAMHIP_DTYPE_INT8) {
-        // int32 GEMM, fp32 h and its row amax in the workspace, then the per-token int8 requantisation
+        // int32 GEMM, fp32 h and its partial row maxima (one per 32 h-columns) in the workspace, then the
+        // per-token int8 requantisation
         CHECK_PARAM(outQuant == CAMHIP_QUANT_INT8_TOKEN, "grouped_matmul_swiglu: int8 inputs need outQuant 2 (got %lld)",
                     (long long)outQuant);
         CHECK_PTR(hScale);
         const uint64_t h_off = 0, amax_off = ((uint64_t)m * (n / 2) * 4 + 255) & ~(uint64_t)255;
-        const uint64_t ws_bytes = amax_off + (uint64_t)m * 4;
+        const uint64_t ws_bytes = amax_off + (uint64_t)m * (n / 2 / cam::GMM_AMAX_COLS) * 4;
         const int L = (int)numGroups, M = (int)m, I = (int)(n / 2);
         const cam::GmmArgs base{(const uint8_t *)x, xScale, groupList, L, M, (int)k, (int)n,
                                 (const uint8_t *)weight, weightScale, nullptr, nullptr};

@@ -76,7 +76,7 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool 
     f.y = c.take(N * H * 2);
     f.inv = c.take(4 * N);
     f.hf = c.take(int8 ? N * I * 4 : 0);  // int8: fp32 h and its row maxima before the requantisation
-    f.amax = c.take(int8 ? N * 4 : 0);
+    f.amax = c.take(int8 ? N * (I / cam::GMM_AMAX_COLS) * 4 : 0);  // partial row maxima of h
     if (shared) {
         f.sh_x = c.take((uint64_t)T * H * esz);
         f.sh_xs = c.take((uint64_t)T * scale_bytes(dt, H));
@@ -84,7 +84,7 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool 
         f.sh_hs = c.take((uint64_t)T * scale_bytes(dt, Ish));
         f.sh_gl = c.take(8);
         f.sh_hf = c.take(int8 ? (uint64_t)T * Ish * 4 : 0);
-        f.sh_amax = c.take(int8 ? (uint64_t)T * 4 : 0);
+        f.sh_amax = c.take(int8 ? (uint64_t)T * (Ish / cam::GMM_AMAX_COLS) * 4 : 0);
     }
     f.bytes = c.off;
     return f;

@@ -6,7 +6,8 @@
 namespace cam {
 
 enum GmmDtype { DT_BF16 = 0, DT_INT8 = 2, DT_FP8 = 3 };
-// EPI_SWIGLU_F32AMAX (int8 only): h in fp32 [M, N/2] and, per row, max |h| over the whole row in Cs[m]
+// EPI_SWIGLU_F32AMAX (int8 only): h in fp32 [M, N/2] and partial row maxima of |h| in Cs [M, N/2/32]: slot
+// c of row m holds max |h| over h-columns [32 c, 32 c + 32), written once by the wave that computed them
 // (float bits, combined across tiles by atomic max; the launcher clears it first), for the per-token
 // int8 requantisation that follows (launch_quant_rows_int8).
 enum GmmEpilogue { EPI_PLAIN = 0, EPI_SWIGLU_BF16 = 1, EPI_SWIGLU_FP8 = 2, EPI_SWIGLU_F32AMAX = 3 };
@@ -32,7 +33,9 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);
 hipError_t launch_scales_to_kmajor(const float *src, const int64_t *group_list, int L, int M, int nb, float *dst,
                                    hipStream_t s);
 // Per-token int8 requantisation of the fp32 h written by EPI_SWIGLU_F32AMAX, rows [0, sum(group_list)):
-// q = rint((h * 127) * (1 / amax)), scale = amax * (1/127); rows with amax 0 get q = 0, scale 0.
+// amax = max of the row's I/32 partial maxima, q = rint((h * 127) * (1 / amax)), scale = amax * (1/127);
+// rows with amax 0 get q = 0, scale 0.
+constexpr int GMM_AMAX_COLS = 32;  // h-columns per partial row maximum
 hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64_t *group_list, int L, int M, int I,
                                   int8_t *q, float *scale, hipStream_t s);
 

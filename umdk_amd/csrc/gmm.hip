@@ -347,8 +347,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                         h[i][j][q] = g / (1.0f + expf(-g)) * u;
                     }
             if constexpr (EPI == EPI_SWIGLU_F32AMAX) {
-                // fp32 h and the row's max |h| over all of its tiles (atomic max on the float bits:
-                // non-negative floats order like their bit patterns)
+                // fp32 h and this wave's partial row maximum of |h| (its 32 h-columns), one slot per wave and
+                // row, so the requantisation needs no zeroed buffer and no atomics
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
                     const int m = row0 + wm * WM + i * 16 + l16;
@@ -366,8 +366,9 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                         for (int j = 0; j < HF; ++j)
                             *reinterpret_cast<f32x4 *>(hrow + 16 * j) =
                                 f32x4{h[i][j][0], h[i][j][1], h[i][j][2], h[i][j][3]};
+                        static_assert(WN / 2 == GMM_AMAX_COLS, "one partial maximum per wave's h-columns");
                         if (lg == 0)
-                            atomicMax(reinterpret_cast<unsigned int *>(p.Cs) + m, __float_as_uint(mx));
+                            p.Cs[(size_t)m * (half_n / GMM_AMAX_COLS) + n0 / GMM_AMAX_COLS + wn] = mx;
                     }
                 }
             } else if constexpr (EPI == EPI_SWIGLU_BF16) {
@@ -914,12 +915,8 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
     } else if (dt == DT_INT8) {
         if (epi == EPI_PLAIN)
             return launch_one<DT_INT8, EPI_PLAIN>(a, s);
-        if (epi == EPI_SWIGLU_F32AMAX) {
-            hipError_t e = launch_fill_i32(reinterpret_cast<int32_t *>(a.Cs), 0, a.M, s);
-            if (e != hipSuccess)
-                return e;
+        if (epi == EPI_SWIGLU_F32AMAX)
             return launch_one<DT_INT8, EPI_SWIGLU_F32AMAX>(a, s);
-        }
     } else if (dt == DT_FP8) {
         if (epi == EPI_PLAIN)
             return launch_one<DT_FP8, EPI_PLAIN>(a, s);
@@ -938,6 +935,7 @@ __global__ __launch_bounds__(256) void quant_rows_int8_kernel(const float *__res
                                                               int I, int8_t *__restrict__ q, float *__restrict__ scale)
 {
     __shared__ int tot;
+    __shared__ float red[256 / 64];
     if (threadIdx.x == 0)
         tot = 0;
     __syncthreads();
@@ -948,8 +946,19 @@ __global__ __launch_bounds__(256) void quant_rows_int8_kernel(const float *__res
         atomicAdd(&tot, part);
     __syncthreads();
     const int total = min(tot, M);
+    const int S = I / GMM_AMAX_COLS;  // partial maxima per row
     for (int m = blockIdx.x; m < total; m += gridDim.x) {
-        const float a = amax_in[m];
+        float pm = 0.0f;
+        for (int c = threadIdx.x; c < S; c += blockDim.x)
+            pm = fmaxf(pm, amax_in[(size_t)m * S + c]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            pm = fmaxf(pm, __shfl_xor(pm, o, 64));
+        if ((threadIdx.x & 63) == 0)
+            red[threadIdx.x >> 6] = pm;
+        __syncthreads();
+        const float a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();  // red is rewritten for the next row
         const float inv = a > 0.0f ? 1.0f / a : 0.0f;  // rows of zeros quantise to 0 with scale 0
         const f32x4 *hr = reinterpret_cast<const f32x4 *>(h + (size_t)m * I);
         uint32_t *qr = reinterpret_cast<uint32_t *>(q + (size_t)m * I);
@@ -969,7 +978,7 @@ __global__ __launch_bounds__(256) void quant_rows_int8_kernel(const float *__res
 hipError_t launch_quant_rows_int8(const float *h, const float *amax, const int64_t *group_list, int L, int M, int I,
                                   int8_t *q, float *scale, hipStream_t s)
 {
-    if (M <= 0 || L <= 0 || (I & 3))
+    if (M <= 0 || L <= 0 || (I % GMM_AMAX_COLS))
         return hipErrorInvalidValue;
     const int grid = M < 4096 ? M : 4096;
     hipLaunchKernelGGL(quant_rows_int8_kernel, dim3(grid), dim3(256), 0, s, h, amax, group_list, L, M, I, q, scale);
