@@ -264,7 +264,7 @@ def test_gmm_fp8_scale_layouts_agree(ops):
 
 
 def test_gmm_bf16_full_mixtral_shape_sampled_rows(ops):
-    # BASELINE config 3 at full size (8 experts, H=4096, I=14336, M=16384, skewed counts); each output row
+    # the Mixtral-8x7B layer at full size (8 experts, H=4096, I=14336, M=16384, skewed counts); each output row
     # depends only on its own input row and its expert's weights, so sampled rows against a torch fp32
     # reference check the whole launch (256-row tiles, every N-tile)
     print("gmm bf16 full Mixtral shape", flush=True)
