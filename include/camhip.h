@@ -49,6 +49,9 @@ typedef struct camhipExecutor camhipExecutor;
 #define CAMHIP_QUANT_NONE 0        /* bf16 rows, scales untouched */
 #define CAMHIP_QUANT_INT8_TOKEN 2  /* int8, one fp32 scale per row (reference use_quant=True) */
 #define CAMHIP_QUANT_FP8_BLOCK 3   /* fp8 e4m3fn, one fp32 scale per 1x128 block (extension) */
+/* the same fp8 rows with the block scales written k-major, [hidden/128, recvRowsCapacity]: the layout the
+ * grouped GEMMs read (xScaleLayout 1), so no transpose runs between dispatch and GMM1 (extension) */
+#define CAMHIP_QUANT_FP8_BLOCK_KMAJOR 5
 
 CAMHIP_API const char *camhipGetLastErrorMsg(void);
 CAMHIP_API const char *camhipGetVersion(void);
@@ -117,14 +120,15 @@ CAMHIP_API camhipStatus camhipNotifyDispatch(void *workspace, uint64_t workspace
  * parity and unused with one rank (may be NULL).
  * Output row of (t,k) = sendOffset[e] + sendTokenIdx[t,k]; rows must fit in
  * recvRowsCapacity.  recvX [rows, hidden]: bf16 (quantMode 0), int8 (2) or
- * fp8 e4m3fn (3).  recvXScales: untouched (0), [rows] (2), [rows, hidden/128] (3).
+ * fp8 e4m3fn (3, 5).  recvXScales: untouched (0), [rows] (2), [rows, hidden/128] (3),
+ * [hidden/128, recvRowsCapacity] (5: element (row, b) at b * recvRowsCapacity + row).
  * assistInfoForCombine [rows, 3] int32 = (epRankId, t, k).
  * waitRecvCostStats (diagnose output, may be NULL): [epWorldSize] int32, per
  * source rank the microseconds the dispatch spent on that rank's rows,
  * accumulated across calls (moe_dispatch_normal.h:489-529); with one rank,
  * entry 0 gains the dispatch phase's time on the stream.
  * Limits (moe_dispatch_normal_tiling.cpp:72-94): hidden in [1024,7168] and a
- * multiple of 16 (of 128 for quantMode 3), numTopk in [1,16], moeExpertNum
+ * multiple of 16 (of 128 for quantMode 3 and 5), numTopk in [1,16], moeExpertNum
  * in [1,512], epWorldSize == 1. */
 CAMHIP_API camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(
     const uint16_t *x, const int32_t *topkIdx, const int32_t *sendOffset, const int32_t *sendTokenIdx,

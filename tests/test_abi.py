@@ -75,7 +75,8 @@ def test_layout_workspace_size_and_short_workspace(L):
     assert st2 == 161003 and "workspace" in L.camhipGetLastErrorMsg().decode()
 
 
-@pytest.mark.parametrize("H,q,frag", [(1000, 0, "hidden"), (8192, 0, "hidden"), (1040, 3, "128"), (1024, 1, "quantMode")])
+@pytest.mark.parametrize("H,q,frag", [(1000, 0, "hidden"), (8192, 0, "hidden"), (1040, 3, "128"), (1040, 5, "128"),
+                                     (1024, 1, "quantMode"), (1024, 4, "quantMode")])
 def test_dispatch_rejects_bad_hidden_and_quant(L, H, q, frag):
     st, _, _, msg = _ws(L, "camhipMoeDispatchNormal", P, P, P, P, None, None, 4, H, 2, 1, 0, 8, q, 8, P, P, P, None)
     assert st == 161001 and frag in msg

@@ -288,3 +288,25 @@ def test_reference_prefill_case_identity_experts(ops, use_quant):
     ref = (x_np * w_np.sum(1, keepdims=True)).astype(np.float64) + 1
     diff = 1 - 2 * (check * ref).sum() / (check * check + ref * ref).sum()
     assert diff < 5e-5
+
+
+def test_dispatch_fp8_kmajor_scales_mode(ops):
+    # quant mode 5 (C ABI): the same fp8 rows, block scales written k-major [H/128, capacity]
+    from umdk_amd import _lib
+    print("dispatch fp8 k-major scales", flush=True)
+    T, H, E, K = 300, 2048, 32, 6
+    x, logits, _ = make_inputs(12, T, H, E, K)
+    idx, w = ops.moe_route(logits.cuda(), None, K)
+    nte, sti = ops.get_dispatch_layout(idx.long(), E, 1)
+    ex, sc, eidx, rc, _ = ops.moe_dispatch_prefill(x.cuda(), idx, w, nte, sti, "ep", 0, 1, True, 3)
+    N = ex.shape[0]
+    cap = N + 7                                   # a capacity above the row count: the k-major stride
+    so = (torch.cumsum(nte, 0) - nte).int()
+    ex5 = torch.empty((cap, H), dtype=torch.float8_e4m3fn, device="cuda")
+    sc5 = torch.full((H // 128, cap), -1.0, device="cuda")
+    ei5 = torch.empty(cap * 3, dtype=torch.int32, device="cuda")
+    _lib.call("camhipMoeDispatchNormal", _lib.ptr(x.cuda()), _lib.ptr(idx), _lib.ptr(so), _lib.ptr(sti.int()), None,
+              None, T, H, K, 1, 0, E, 5, cap, _lib.ptr(ex5), _lib.ptr(sc5), _lib.ptr(ei5), None, device="cuda")
+    assert torch.equal(ex5[:N].view(torch.uint8), ex.view(torch.uint8))
+    assert torch.equal(sc5[:, :N].t(), sc)
+    assert torch.equal(ei5[:3 * N], eidx)

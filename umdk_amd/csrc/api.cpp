@@ -251,8 +251,11 @@ camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(const uint16_t *x, const in
     CHECK_PARAM(moeExpertNum >= 1 && moeExpertNum <= kMaxExperts, "moe_dispatch: moeExpertNum %lld out of range",
                 (long long)moeExpertNum);
     CHECK_PARAM(quantMode == CAMHIP_QUANT_NONE || quantMode == CAMHIP_QUANT_INT8_TOKEN ||
-                    quantMode == CAMHIP_QUANT_FP8_BLOCK,
-                "moe_dispatch: quantMode %lld not supported (0, 2 or 3)", (long long)quantMode);
+                    quantMode == CAMHIP_QUANT_FP8_BLOCK || quantMode == CAMHIP_QUANT_FP8_BLOCK_KMAJOR,
+                "moe_dispatch: quantMode %lld not supported (0, 2, 3 or 5)", (long long)quantMode);
+    const bool kmajor = quantMode == CAMHIP_QUANT_FP8_BLOCK_KMAJOR;
+    if (kmajor)
+        quantMode = CAMHIP_QUANT_FP8_BLOCK;
     CHECK_PARAM(quantMode != CAMHIP_QUANT_FP8_BLOCK || hidden % 128 == 0,
                 "moe_dispatch: fp8 1x128 quantisation needs hidden %% 128 == 0 (hidden %lld)", (long long)hidden);
     CHECK_PARAM(recvRowsCapacity >= 0, "moe_dispatch: negative recvRowsCapacity");
@@ -280,7 +283,7 @@ camhipStatus camhipMoeDispatchNormalGetWorkspaceSize(const uint16_t *x, const in
                     return e;
             }
             hipError_t e = cam::launch_dispatch(x, topkIdx, sendOffset, sendTokenIdx, T, H, K, E, rank, cap, q, recvX,
-                                                recvXScales, assistInfoForCombine, s);
+                                                recvXScales, assistInfoForCombine, s, nullptr, nullptr, kmajor);
             if (e != hipSuccess || !stats)
                 return e;
             return cam::launch_phase_end((const uint64_t *)w, stats, rank, s);

@@ -52,6 +52,7 @@ _impl = torch.library.Library(LIB_NAME, "IMPL", "CUDA")
 _meta = torch.library.Library(LIB_NAME, "IMPL", "Meta")
 
 QUANT_NONE, QUANT_INT8_TOKEN, QUANT_FP8_BLOCK = 0, 2, 3
+QUANT_FP8_BLOCK_KMAJOR = 5  # C-ABI dispatch only: fp8 rows with k-major block scales (the GEMMs' layout)
 
 
 def _check(cond, msg):

@@ -10,7 +10,7 @@ and can be captured in a HIP graph.  Rows past recv_count[-1] are unused.
 import torch
 
 from . import _lib
-from .ops import QUANT_FP8_BLOCK, QUANT_INT8_TOKEN, QUANT_NONE
+from .ops import QUANT_FP8_BLOCK, QUANT_FP8_BLOCK_KMAJOR, QUANT_INT8_TOKEN, QUANT_NONE
 
 
 class MoePrefillPlan:
@@ -102,6 +102,9 @@ class MoeLayerPlan(MoePrefillPlan):
         dev = self.device
         N = self.N
         if dtype == "fp8":
+            # the dispatch writes the block scales k-major ([H/128, N] storage), the layout GMM1 reads directly
+            self.q = QUANT_FP8_BLOCK_KMAJOR
+            self.scales = torch.empty((H // 128, N), dtype=torch.float32, device=dev).t()
             self.h = torch.empty((N, I), dtype=torch.float8_e4m3fn, device=dev)
             # k-major h scales ([I/128, N] storage): GMM1 writes and GMM2 reads this layout
             self.h_scale = torch.empty((I // 128, N), dtype=torch.float32, device=dev).t()
@@ -109,10 +112,6 @@ class MoeLayerPlan(MoePrefillPlan):
             self.h = torch.empty((N, I), dtype=torch.bfloat16, device=dev)
             self.h_scale = None
         self.y = torch.empty((N, H), dtype=torch.bfloat16, device=dev)
-        # GMM1 transposes the dispatch's row-major fp8 scales into this workspace
-        ws1 = _lib.workspace_size("camhipGroupedMatmulSwiglu", 1, 1, 1, L, N, H, 2 * I, 1, 1,
-                                  3 if dtype == "fp8" else 0, 0, 3 if dtype == "fp8" else 0, 1, 1)
-        self.ws_gmm1 = torch.empty(max(ws1, 1), dtype=torch.uint8, device=dev)
         self.topk_idx = torch.empty((T, K), dtype=torch.int32, device=dev)
 
     def route(self, logits, bias=None, stream=None):
@@ -129,9 +128,8 @@ class MoeLayerPlan(MoePrefillPlan):
         xs = self.scales.data_ptr() if self.dtype == "fp8" else None
         _lib.launch("camhipGroupedMatmulSwiglu", self.expand_x.data_ptr(), xs,
                     self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.H, 2 * self.I, w1.data_ptr(),
-                    None if w1_scale is None else w1_scale.data_ptr(), dt, 0, 3 if dt == 3 else 0, self.h.data_ptr(),
-                    None if self.h_scale is None else self.h_scale.data_ptr(), workspace=self.ws_gmm1,
-                    stream=stream, device=self.device)
+                    None if w1_scale is None else w1_scale.data_ptr(), dt, 1, 3 if dt == 3 else 0, self.h.data_ptr(),
+                    None if self.h_scale is None else self.h_scale.data_ptr(), stream=stream, device=self.device)
         return self.h
 
     def gmm2(self, w2, w2_scale, stream=None):
