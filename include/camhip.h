@@ -246,7 +246,7 @@ CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceS
  * local expert).  L = moeExpertNum / epRankSize; epRankSize must be 1 here.
  * quantMode is reserved (0), as in the reference.  Limits
  * (fused_deep_moe_tiling.cpp:59-75, widened where the GPU allows): batchSize
- * <= 4096, topK <= 12, hidden in [1024,7168] and % 256 == 0, gmm1HiddenSize % 256 == 0. */
+ * <= 4096, topK <= 12, hidden in [512,7168] and % 256 == 0 (the reference fused tiling's smallest token length is 512), gmm1HiddenSize % 256 == 0. */
 CAMHIP_API camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
     const uint16_t *x, const int32_t *expertIds, const void *gmm1Weight, const float *gmm1WeightScale,
     const void *gmm2Weight, const float *gmm2WeightScale, const float *expertScales, const void *shareGmm1Weight,

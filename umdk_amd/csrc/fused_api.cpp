@@ -130,8 +130,9 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
     F_CHECK(topK >= 1 && topK <= 12, "fused_deep_moe: topk %lld out of [1,12]", (long long)topK);
     F_CHECK(moeExpertNum >= 1 && moeExpertNum <= 512 && topK <= moeExpertNum,
             "fused_deep_moe: moe_expert_num %lld out of [topk,512]", (long long)moeExpertNum);
-    F_CHECK(hidden >= 1024 && hidden <= 7168 && hidden % 256 == 0,
-            "fused_deep_moe: hidden %lld must be in [1024,7168] and a multiple of 256", (long long)hidden);
+    // the reference's fused tiling accepts token lengths from 512 (fused_deep_moe_tiling.cpp:66-67)
+    F_CHECK(hidden >= 512 && hidden <= 7168 && hidden % 256 == 0,
+            "fused_deep_moe: hidden %lld must be in [512,7168] and a multiple of 256", (long long)hidden);
     F_CHECK(gmm1HiddenSize >= 256 && gmm1HiddenSize % 256 == 0,
             "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
     F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_INT8 || weightDtype == CAMHIP_DTYPE_FP8,
