@@ -91,6 +91,7 @@ def cpu_baseline(T, H, E, K, seed):
 
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, POP/s
 
 
 def zipf_bias(E, s, seed):
@@ -173,10 +174,10 @@ def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
     counts = plan.recv_tokens_per_expert[:L].cpu()
     M = int(counts.sum())
     touched = int((counts > 0).sum())
-    esz = 1 if dtype == "fp8" else 2
+    esz = 1 if dtype in ("fp8", "int8") else 2
     f1, f2 = 2.0 * M * H * 2 * I, 2.0 * M * I * H
     wb1, wb2 = touched * 2 * I * H * esz, touched * H * I * esz
-    peak = FP8_PEAK_TFLOPS if dtype == "fp8" else BF16_PEAK_TFLOPS
+    peak = {"fp8": FP8_PEAK_TFLOPS, "int8": INT8_PEAK_TOPS}.get(dtype, BF16_PEAK_TFLOPS)
     # roofline time per GEMM: max(FLOP/peak, weight+activation bytes/HBM peak)
     ab1 = M * H * esz + M * I * esz + wb1
     ab2 = M * I * esz + M * H * 2 + wb2
@@ -332,7 +333,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "5", "5i8", "sweep", "peaks", "all"],
+    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "4i8", "5", "5i8", "sweep", "peaks", "all"],
                     help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
                          "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; peaks: measured copy/read bandwidth and vendor GEMM rates; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
     ap.add_argument("--sweep-m", type=int, default=0, help="--config sweep: only this M")
@@ -357,13 +358,15 @@ def main():
 
     cfg3 = lambda st, wu: run_layer("config3: Mixtral-8x7B grouped SwiGLU FFN, bf16", 8192, 4096, 8, 2, 8, 14336,
                                     "bf16", st, wu, args.seed, None)
-    cfg4 = lambda st, wu: run_layer("config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), fp8",
-                                    4096, 7168, 256, 8, 32, 2048, "fp8", st, wu, args.seed, "zipf")
+    cfg4 = lambda st, wu, dt="fp8": run_layer(
+        f"config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), {dt}", 4096, 7168, 256, 8, 32, 2048,
+        dt, st, wu, args.seed, "zipf")
     if args.config == "peaks":
         print(json.dumps({"config": "peaks", "result": measured_peaks()}))
         return
-    if args.config in ("3", "4", "5", "5i8", "sweep"):
+    if args.config in ("3", "4", "4i8", "5", "5i8", "sweep"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
+             "4i8": lambda: cfg4(args.steps, args.warmup, "int8"),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed),
              "5i8": lambda: run_decode(max(args.steps, 1000), args.seed, "int8"),
              "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
@@ -450,6 +453,7 @@ def main():
         result["config3"] = cfg3(10, 3)
         torch.cuda.empty_cache()
         result["config4"] = cfg4(20, 5)
+        result["config4_int8"] = cfg4(20, 5, "int8")
         torch.cuda.empty_cache()
         result["config5"] = run_decode(1000, args.seed)
         torch.cuda.empty_cache()

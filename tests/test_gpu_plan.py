@@ -28,16 +28,16 @@ def _weights(L, H, I, dtype):
 
 def _chain(ops, plan, x, w1, s1, w2, s2, dtype, E_local):
     # the small-op chain on the plan's own routing (ids of non-local experts are not routed here)
-    fp8 = dtype == "fp8"
+    q = {"bf16": 0, "int8": 2, "fp8": 3}[dtype]
     ids = plan.topk_idx.clone()
     nte, sti = ops.get_dispatch_layout(ids.long(), E_local, 1)
-    ex, xs, eidx, rc, rtpe = ops.moe_dispatch_prefill(x, ids, plan.topk_w, nte, sti, "ep", 0, 1, fp8, 3 if fp8 else 0)
-    h, hs = ops.grouped_matmul_swiglu(ex, xs if fp8 else None, rtpe, w1, s1, 3 if fp8 else 0)
-    y = ops.grouped_matmul(h, hs if fp8 else None, rtpe, w2, s2)
+    ex, xs, eidx, rc, rtpe = ops.moe_dispatch_prefill(x, ids, plan.topk_w, nte, sti, "ep", 0, 1, q != 0, q)
+    h, hs = ops.grouped_matmul_swiglu(ex, xs if q else None, rtpe, w1, s1, q)
+    y = ops.grouped_matmul(h, hs if q else None, rtpe, w2, s2)
     return ops.moe_combine_prefill(y, ids, plan.topk_w, eidx, rc, "ep", 0, 1), rtpe
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp8", "int8"])
 def test_layer_plan_matches_op_chain_and_replays(ops, dtype):
     from umdk_amd.plan import MoeLayerPlan
     print(f"layer plan {dtype}", flush=True)

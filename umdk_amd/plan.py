@@ -90,12 +90,18 @@ class MoeLayerPlan(MoePrefillPlan):
 
     dtype "bf16": bf16 rows and weights, bf16 h.  dtype "fp8": fp8 e4m3fn rows
     with 1x128 scales, fp8 weights with 128x128 scales, fp8 h with 1x128
-    scales; the output is bf16 either way.  Weights are [L, 2I, H] and
-    [L, H, I] with the reduction dimension contiguous.
+    scales.  dtype "int8": the reference's int8 prefill numerics -- int8 rows
+    with per-token scales (the use_quant recipe, moe_dispatch_normal.h:295-332),
+    int8 weights with per-output-channel scales [L, 2I] / [L, H], int8 h
+    requantised per token.  The output is bf16 in every mode.  Weights are
+    [L, 2I, H] and [L, H, I] with the reduction dimension contiguous.
     """
 
     def __init__(self, T, H, E, K, L, I, dtype="fp8", device="cuda"):
-        q = QUANT_FP8_BLOCK if dtype == "fp8" else QUANT_NONE
+        _check = {"bf16": QUANT_NONE, "fp8": QUANT_FP8_BLOCK, "int8": QUANT_INT8_TOKEN}
+        if dtype not in _check:
+            raise ValueError(f"MoeLayerPlan: dtype must be bf16, fp8 or int8 (got {dtype})")
+        q = _check[dtype]
         self.E_route = E
         super().__init__(T, H, L, K, quant_mode=q, device=device)
         self.L, self.I, self.dtype = L, I, dtype
@@ -108,10 +114,17 @@ class MoeLayerPlan(MoePrefillPlan):
             self.h = torch.empty((N, I), dtype=torch.float8_e4m3fn, device=dev)
             # k-major h scales ([I/128, N] storage): GMM1 writes and GMM2 reads this layout
             self.h_scale = torch.empty((I // 128, N), dtype=torch.float32, device=dev).t()
+        elif dtype == "int8":
+            self.h = torch.empty((N, I), dtype=torch.int8, device=dev)
+            self.h_scale = torch.empty(N, dtype=torch.float32, device=dev)
         else:
             self.h = torch.empty((N, I), dtype=torch.bfloat16, device=dev)
             self.h_scale = None
         self.y = torch.empty((N, H), dtype=torch.bfloat16, device=dev)
+        # int8 GMM1 keeps its fp32 h and partial row maxima in a workspace until the per-token requantisation
+        ws1 = _lib.workspace_size("camhipGroupedMatmulSwiglu", 1, 1, 1, L, N, H, 2 * I, 1, 1, self._dt(), 0,
+                                  self._out_quant(), 1, 1)
+        self.ws_gmm1 = torch.empty(max(ws1, 1), dtype=torch.uint8, device=dev) if ws1 else None
         self.topk_idx = torch.empty((T, K), dtype=torch.int32, device=dev)
 
     def route(self, logits, bias=None, stream=None):
@@ -123,22 +136,29 @@ class MoeLayerPlan(MoePrefillPlan):
         self.gmm1(w1, w1_scale, stream)
         return self.gmm2(w2, w2_scale, stream)
 
+    def _dt(self):
+        return {"bf16": 0, "int8": 2, "fp8": 3}[self.dtype]
+
+    def _out_quant(self):
+        return {"bf16": QUANT_NONE, "int8": QUANT_INT8_TOKEN, "fp8": QUANT_FP8_BLOCK}[self.dtype]
+
     def gmm1(self, w1, w1_scale, stream=None):
-        dt = 3 if self.dtype == "fp8" else 0
-        xs = self.scales.data_ptr() if self.dtype == "fp8" else None
+        dt = self._dt()
+        xs = self.scales.data_ptr() if dt else None
         _lib.launch("camhipGroupedMatmulSwiglu", self.expand_x.data_ptr(), xs,
                     self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.H, 2 * self.I, w1.data_ptr(),
-                    None if w1_scale is None else w1_scale.data_ptr(), dt, 1, 3 if dt == 3 else 0, self.h.data_ptr(),
-                    None if self.h_scale is None else self.h_scale.data_ptr(), stream=stream, device=self.device)
+                    None if w1_scale is None else w1_scale.data_ptr(), dt, 1 if dt == 3 else 0, self._out_quant(),
+                    self.h.data_ptr(), None if self.h_scale is None else self.h_scale.data_ptr(),
+                    workspace=self.ws_gmm1, stream=stream, device=self.device)
         return self.h
 
     def gmm2(self, w2, w2_scale, stream=None):
-        dt = 3 if self.dtype == "fp8" else 0
+        dt = self._dt()
         _lib.launch("camhipGroupedMatmul", self.h.data_ptr(),
                     None if self.h_scale is None else self.h_scale.data_ptr(),
                     self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.I, self.H, w2.data_ptr(),
-                    None if w2_scale is None else w2_scale.data_ptr(), dt, 1, self.y.data_ptr(), stream=stream,
-                    device=self.device)
+                    None if w2_scale is None else w2_scale.data_ptr(), dt, 1 if dt == 3 else 0, self.y.data_ptr(),
+                    stream=stream, device=self.device)
         return self.y
 
     def forward(self, x, logits, bias, w1, w1_scale, w2, w2_scale, stream=None):
