@@ -187,6 +187,12 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
 #define CAMHIP_DTYPE_BF16 0
 #define CAMHIP_DTYPE_INT8 2
 #define CAMHIP_DTYPE_FP8 3
+/* OR'ed into camhipFusedDeepMoe's weightDtype: separated weights, the reference's per-expert
+ * tensor lists (pybind/fused_deep_moe.cpp:33-36, TensorList gmm1Weight ...; dynamic EPLB,
+ * test_fused_deep_moe.py:256-269).  gmm1Weight, gmm1WeightScale, gmm2Weight and
+ * gmm2WeightScale then each point to a device array of L device pointers, entry e being
+ * expert e's [n, k] weight (k contiguous) or its scales ([n/128, k/128] fp8, [n] int8). */
+#define CAMHIP_WEIGHT_LIST 0x100
 
 /* GMM1 + SwiGLU: n = 2I, weight rows [0,I) gate, [I,2I) up;
  * h[m, I] = silu(x W_gate^T) * (x W_up^T), silu(g) = g / (1 + exp(-g))
@@ -228,7 +234,7 @@ CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceS
  * x [batchSize, hidden] bf16; expertIds [batchSize, topK] int32 in
  * [-1, moeExpertNum) (-1: placeholder, not routed); expertScales [batchSize, topK]
  * fp32 combine weights; xActiveMask [batchSize] bool (1 byte, true prefix) or NULL.
- * Weights in coupled mode with the reduction dimension contiguous:
+ * Weights in coupled mode (or separated: CAMHIP_WEIGHT_LIST) with the reduction dimension contiguous:
  * gmm1Weight [L, gmm1HiddenSize, hidden] (rows [0,I) gate, [I,2I) up),
  * gmm2Weight [L, hidden, gmm1HiddenSize/2]; weightDtype CAMHIP_DTYPE_BF16,
  * CAMHIP_DTYPE_FP8 with block scales [L, n/128, k/128] (activations are then

@@ -193,6 +193,66 @@ def test_fused_graph_capture_replays(ops):
         del junk
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_fused_separated_allocations_in_place(ops, dtype):
+    # dynamic-EPLB weights (test_fused_deep_moe.py:256-269): one allocation per expert, made in a
+    # scrambled order, weights and scales both as lists.  The op reads them in place through device
+    # pointer tables: bit-identical to the coupled call, no stacked copy of the weights, and a graph
+    # captured on the lists replays correctly.
+    bs, H, I, E, K = 128, 7168, 256, 32, 8
+    d = make(7, bs, H, I, E, K, dtype)
+    ref, _, etn_ref = call_fused(ops, d, E)
+    order = torch.randperm(E, generator=torch.Generator().manual_seed(1)).tolist()
+    g1, g2, s1, s2 = [None] * E, [None] * E, [None] * E, [None] * E
+    for e in order:
+        g1[e] = d["w1"][e].clone().transpose(0, 1)       # logical [H, 2I] over k-contiguous storage
+        g2[e] = d["w2"][e].clone().transpose(0, 1)
+        if dtype == "fp8":
+            s1[e] = d["s1"][e].clone()
+            s2[e] = d["s2"][e].clone()
+    if dtype != "fp8":
+        s1 = s2 = []
+    call = lambda: ops.fused_deep_moe(d["x"], d["ids"], g1, s1, g2, s2, d["scales"], None, None, None, None,  # noqa: E731
+                                      None, None, None, "ep", 1, 0, E, 0, 0)
+    torch.cuda.synchronize()
+    wbytes = sum(t.numel() * t.element_size() for t in g1 + g2)
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    out, _, etn = call()
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated() - base < wbytes // 4   # workspace and outputs only
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)) and torch.equal(etn, etn_ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, _, getn = call()
+    for r in range(3):
+        junk = torch.randn(1 << 20, device="cuda") * r
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout.view(torch.int16), ref.view(torch.int16)), f"replay {r}"
+        assert torch.equal(getn, etn_ref)
+        del junk
+
+
+def test_fused_rejects_bad_weight_lists(ops):
+    d = make(2, 8, 1024, 128, 8, 2, "bf16")
+    g1 = list(d["w1"].transpose(1, 2).unbind(0))
+    g2 = list(d["w2"].transpose(1, 2).unbind(0))
+    with pytest.raises(RuntimeError, match="per-expert tensors"):
+        ops.fused_deep_moe(d["x"], d["ids"], g1[:7], [], g2, [], d["scales"], None, None, None, None, None, None,
+                           None, "ep", 1, 0, 8, 0, 0)
+    with pytest.raises(RuntimeError, match="logical shape"):
+        bad = g1[:7] + [torch.zeros(1024, 128, dtype=torch.bfloat16, device="cuda")]
+        ops.fused_deep_moe(d["x"], d["ids"], bad, [], g2, [], d["scales"], None, None, None, None, None, None,
+                           None, "ep", 1, 0, 8, 0, 0)
+
+
 def test_fused_rejects_unsupported(ops):
     d = make(1, 4, 1024, 128, 8, 2, "bf16")
     with pytest.raises(RuntimeError, match="one EP rank"):

@@ -135,6 +135,10 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
             "fused_deep_moe: hidden %lld must be in [512,7168] and a multiple of 256", (long long)hidden);
     F_CHECK(gmm1HiddenSize >= 256 && gmm1HiddenSize % 256 == 0,
             "fused_deep_moe: gmm1 hidden size (2I) %lld must be a multiple of 256", (long long)gmm1HiddenSize);
+    // separated mode (the reference's per-expert tensor lists, dynamic EPLB): the four routed-expert weight
+    // arguments are device arrays of L pointers
+    const bool wlist = (weightDtype & CAMHIP_WEIGHT_LIST) != 0;
+    weightDtype &= ~(int64_t)CAMHIP_WEIGHT_LIST;
     F_CHECK(weightDtype == CAMHIP_DTYPE_BF16 || weightDtype == CAMHIP_DTYPE_INT8 || weightDtype == CAMHIP_DTYPE_FP8,
             "fused_deep_moe: weight dtype %lld not supported (bf16, int8 or fp8 e4m3fn)", (long long)weightDtype);
     F_CHECK(quantMode == 0, "fused_deep_moe: quant_mode is reserved and must be 0 (got %lld)", (long long)quantMode);
@@ -219,9 +223,17 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
                                      expertSmoothScales, true));
         cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
                         (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
+        if (wlist) {
+            g1.Wl = (const uint8_t *const *)gmm1Weight;
+            g1.Wsl = (const float *const *)gmm1WeightScale;
+        }
         HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), s));
         cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
                         (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
+        if (wlist) {
+            g2.Wl = (const uint8_t *const *)gmm2Weight;
+            g2.Wsl = (const float *const *)gmm2WeightScale;
+        }
         HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
         HIP_TRY(cam::launch_combine_gather((const uint16_t *)P(f.y), (const int32_t *)P(f.eidx), N,
                                            recv_cnt + (L - 1), expertScales, T, K, H, output,

@@ -25,6 +25,10 @@ struct GmmArgs {
     uint8_t *C;                 // plain: bf16 [M, N]; SwiGLU: h [M, N/2] (bf16, fp8 or fp32)
     float *Cs;                  // SwiGLU fp8: [N/256, M] h block scales (k-major); SwiGLU fp32: [M] row max |h|
     int allow256 = 1;           // set by the launcher: the 256-row tile may be picked on the device
+    // Separated weights (optional): device arrays of L pointers, expert e's [N, K] weight and its scales
+    // ([N/128, K/128] fp8, [N] int8); when set, W and Ws are not read.
+    const uint8_t *const *Wl = nullptr;
+    const float *const *Wsl = nullptr;
 };
 
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);

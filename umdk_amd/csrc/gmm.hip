@@ -237,6 +237,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
     struct Ctx {
         int e, row0, seg1, n0;
         const uint8_t *wbase;
+        const float *wsb;  // this expert's weight scales (fp8 block or int8 per-channel), or null
         uint32_t ga[A_LOADS], gb[B_LOADS], gs[TC::S_DMAS];
         int wsg, wsu;  // fp8: weight-scale row offsets (gate / up n-blocks, or the wave's column block)
         bool active;   // some row of this wave lies inside the segment
@@ -268,7 +269,13 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
         // DMA and meets every barrier): a tile of a short segment costs little more than its weights
         c.active = c.row0 + wm * WM < c.seg1;
-        c.wbase = p.W + (size_t)e * p.N * kbytes;
+        if (p.Wl) {  // separated weights: one allocation per expert
+            c.wbase = p.Wl[e];
+            c.wsb = p.Wsl ? p.Wsl[e] : nullptr;
+        } else {
+            c.wbase = p.W + (size_t)e * p.N * kbytes;
+            c.wsb = !p.Ws ? nullptr : p.Ws + (INT8 ? (size_t)e * p.N : (size_t)e * (p.N / 128) * nk);
+        }
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
             const int r = (i * NW + w) * 8 + band_row;  // tile row 0..GBM-1
@@ -293,9 +300,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
 #pragma unroll
         for (int d = 0; d < TC::S_DMAS; ++d)
             c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, p.M - 1);  // k-major: + kc * M
-        const int nb = p.N / 128;
-        c.wsg = (e * nb + (SWIGLU ? c.n0 : c.n0 + wn * WN) / 128) * nk;
-        c.wsu = SWIGLU ? (e * nb + (half_n + c.n0) / 128) * nk : c.wsg;
+        c.wsg = ((SWIGLU ? c.n0 : c.n0 + wn * WN) / 128) * nk;
+        c.wsu = SWIGLU ? ((half_n + c.n0) / 128) * nk : c.wsg;
     };
     // DMA instruction q (0 <= q < LOADS) of k-step kc of tile c into ring slot `slot`: A bands, then
     // W bands, then (fp8) the activation scales
@@ -484,7 +490,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                         b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                      (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                     }
-                    const float sg = sload(p.Ws, c.wsg + ks), su = SWIGLU ? sload(p.Ws, c.wsu + ks) : sg;
+                    const float sg = sload(c.wsb, c.wsg + ks), su = SWIGLU ? sload(c.wsb, c.wsu + ks) : sg;
                     const int kn = min(ks + 1, nk - 1);  // past the end: reload the last k-step
 #pragma unroll
                     for (int i = 0; i < AHEAD; ++i)
@@ -622,8 +628,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                                        (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                     }
                     const int kc = min(ks, nk - 1);
-                    r.sg = sload(p.Ws, cur.wsg + kc);
-                    r.su = SWIGLU ? sload(p.Ws, cur.wsu + kc) : r.sg;
+                    r.sg = sload(cur.wsb, cur.wsg + kc);
+                    r.su = SWIGLU ? sload(cur.wsb, cur.wsu + kc) : r.sg;
                 };
                 auto rd_a = [&](int i, int ks) {
                     const uint8_t *st = stage_ptr(ks);
@@ -750,7 +756,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             if constexpr (INT8) {
                 // per-channel x per-token dequantisation of the exact int32 sums:
                 // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
-                const float *wsr = p.Ws + (size_t)cur.e * p.N;
+                const float *wsr = cur.wsb;
 #pragma unroll
                 for (int j = 0; j < JF; ++j) {
                     int c0;

@@ -52,6 +52,7 @@ _impl = torch.library.Library(LIB_NAME, "IMPL", "CUDA")
 _meta = torch.library.Library(LIB_NAME, "IMPL", "Meta")
 
 QUANT_NONE, QUANT_INT8_TOKEN, QUANT_FP8_BLOCK = 0, 2, 3
+WEIGHT_LIST = 0x100  # OR'ed into the fused entry's weight dtype: per-expert weight pointer tables
 QUANT_FP8_BLOCK_KMAJOR = 5  # C-ABI dispatch only: fp8 rows with k-major block scales (the GEMMs' layout)
 
 
@@ -295,33 +296,87 @@ def _kmajor(w, n, k, what):
     raise RuntimeError(f"fused_deep_moe: {what} must have logical shape [..., {k}, {n}], got {tuple(w.shape)}")
 
 
+def _is_coupled(ws):
+    return len(ws) == 1 and ws[0].dim() == 3
+
+
 def _coupled(ws, L, n, k, what):
-    if len(ws) == 1 and ws[0].dim() == 3:
-        w = _kmajor(ws[0], n, k, what)
-    else:
-        _check(len(ws) == L, f"fused_deep_moe: {what} needs 1 coupled tensor or {L} per-expert tensors")
-        w = torch.stack([_kmajor(t, n, k, what) for t in ws])   # separated mode: one copy per call
+    w = _kmajor(ws[0], n, k, what)
     _check(tuple(w.shape) == (L, n, k), f"fused_deep_moe: {what} shape mismatch")
     return w.contiguous()
 
 
 def _scales(ss, L, n, k, what):
-    """fp8 128x128 block scales [L, n/128, k/128] (one coupled tensor or L per-expert ones)."""
+    """fp8 128x128 block scales [L, n/128, k/128] (one coupled tensor)."""
     if not ss or ss[0] is None:
         return None
-    s = ss[0] if (len(ss) == 1 and ss[0].dim() == 3) else torch.stack(list(ss))
-    _check(s.dtype == torch.float32 and tuple(s.shape) == (L, n // 128, k // 128),
+    s = ss[0]
+    _check(s.dim() == 3 and s.dtype == torch.float32 and tuple(s.shape) == (L, n // 128, k // 128),
            f"fused_deep_moe: {what} must be float32 [{L}, {n // 128}, {k // 128}] (128x128 block scales)")
     return s.contiguous()
 
 
 def _channel_scales(ss, L, n, what):
-    """int8 per-channel scales [L, n] (coupled) or L tensors of [n]; cast to float32 as the
-    reference's test builds them in float (test_fused_deep_moe.py:309-312)."""
+    """int8 per-channel scales [L, n] (one coupled tensor); cast to float32 as the reference's
+    test builds them in float (test_fused_deep_moe.py:309-312)."""
     _check(bool(ss) and ss[0] is not None, f"fused_deep_moe: int8 weights need {what}")
-    s = ss[0] if (len(ss) == 1 and ss[0].dim() == 2) else torch.stack(list(ss))
-    _check(tuple(s.shape) == (L, n), f"fused_deep_moe: {what} must be [{L}, {n}] per-channel scales")
+    s = ss[0]
+    _check(s.dim() == 2 and tuple(s.shape) == (L, n), f"fused_deep_moe: {what} must be [{L}, {n}] per-channel scales")
     return s.to(torch.float32).contiguous()
+
+
+def _per_expert(ws, L, what, coupled_dim):
+    """The L per-expert tensors of a weight argument: the reference's separated lists as given, or
+    the slices of one coupled tensor (views, no copy)."""
+    _check(bool(ws) and ws[0] is not None, f"fused_deep_moe: {what} missing")
+    if len(ws) == 1 and ws[0].dim() == coupled_dim:
+        _check(ws[0].shape[0] == L, f"fused_deep_moe: {what} holds {ws[0].shape[0]} experts, need {L}")
+        return list(ws[0].unbind(0))
+    _check(len(ws) == L, f"fused_deep_moe: {what} needs 1 coupled tensor or {L} per-expert tensors, got {len(ws)}")
+    return list(ws)
+
+
+_PTR_TABLES = {}
+
+
+def _ptr_table(ts, device):
+    """Device array of the tensors' data pointers (int64), cached by the pointer values so that a
+    steady caller (and a captured graph) reuses one table."""
+    key = (str(device),) + tuple(t.data_ptr() for t in ts)
+    tab = _PTR_TABLES.get(key)
+    if tab is None:
+        if len(_PTR_TABLES) >= 64:
+            _PTR_TABLES.clear()
+        tab = torch.tensor(key[1:], dtype=torch.int64).to(device)
+        _PTR_TABLES[key] = tab
+    return tab
+
+
+def _separated(ws, ss, L, n, k, fp8, int8, what, device):
+    """Separated mode (the reference's per-expert TensorList weights, dynamic EPLB:
+    test_fused_deep_moe.py:256-269): no stacking copy; the kernels read each expert through a
+    device pointer table.  Returns (weight table, scale table or None, tensors to keep alive)."""
+    we = [_kmajor(t, n, k, what) for t in _per_expert(ws, L, what, 3)]
+    for t in we:
+        _check(tuple(t.shape) == (n, k) and t.is_contiguous() and t.device == device,
+               f"fused_deep_moe: each {what} must be [{k}, {n}] with one expert per tensor on {device}")
+    keep = list(we)
+    st = None
+    if fp8 or int8:
+        sname = what + "_scale"
+        se = _per_expert(ss, L, sname, 3 if fp8 else 2)
+        if fp8:
+            se = [t.contiguous() for t in se]
+            for t in se:
+                _check(t.dtype == torch.float32 and tuple(t.shape) == (n // 128, k // 128),
+                       f"fused_deep_moe: each {sname} must be float32 [{n // 128}, {k // 128}]")
+        else:
+            se = [t.to(torch.float32).contiguous().view(-1) for t in se]
+            for t in se:
+                _check(t.numel() == n, f"fused_deep_moe: each {sname} must have {n} per-channel scales")
+        keep += se
+        st = _ptr_table(se, device)
+    return _ptr_table(we, device), st, keep
 
 
 def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, gmm2_weight_scale, expert_scales,
@@ -333,8 +388,9 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
 
     Mirrors FusedDeepMoeImplNpu (pybind/fused_deep_moe.cpp:30-83) and the API
     guide (doc/en/cam/CAM API Guide.md:177-226): weights in the logical
-    [L, H, 2I] / [L, I, H] shapes (one coupled tensor or L separated ones;
-    a transposed view of k-contiguous storage avoids a copy), expert_ids
+    [L, H, 2I] / [L, I, H] shapes (one coupled tensor, or L separated ones
+    read in place through device pointer tables; a transposed view of
+    k-contiguous storage avoids a copy), expert_ids
     int32 with -1 placeholders, x_active_mask a true-prefix bool mask.
     Weights are int8 with per-channel scales [L, 2I] / [L, H] -- the
     reference's own mode, with optional smooth-quant scales
@@ -355,12 +411,21 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
     w1_logical = gmm1_weight[0].shape
     n1 = w1_logical[-1]
     I = n1 // 2
-    w1 = _coupled(gmm1_weight, L, n1, h, "gmm1_weight")
-    w2 = _coupled(gmm2_weight, L, h, I, "gmm2_weight")
     fp8 = dt == torch.float8_e4m3fn
     int8 = dt == torch.int8
+    separated = not (_is_coupled(gmm1_weight) and _is_coupled(gmm2_weight))
     s1 = s2 = None
-    if fp8:
+    keep = []
+    if separated:
+        w1, s1, k1 = _separated(gmm1_weight, gmm1_weight_scale, L, n1, h, fp8, int8, "gmm1_weight", x.device)
+        w2, s2, k2 = _separated(gmm2_weight, gmm2_weight_scale, L, h, I, fp8, int8, "gmm2_weight", x.device)
+        keep = k1 + k2  # noqa: F841 -- per-expert tensors stay alive until the launch is queued
+    else:
+        w1 = _coupled(gmm1_weight, L, n1, h, "gmm1_weight")
+        w2 = _coupled(gmm2_weight, L, h, I, "gmm2_weight")
+    if separated:
+        pass  # tables built above
+    elif fp8:
         s1 = _scales(gmm1_weight_scale, L, n1, h, "gmm1_weight_scale")
         s2 = _scales(gmm2_weight_scale, L, h, I, "gmm2_weight_scale")
     elif int8:
@@ -407,7 +472,7 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
     _lib.call("camhipFusedDeepMoe", _lib.ptr(x), _lib.ptr(ids), _lib.ptr(w1), _lib.ptr(s1), _lib.ptr(w2),
               _lib.ptr(s2), _lib.ptr(es), _lib.ptr(sw1), _lib.ptr(ss1), _lib.ptr(sw2), _lib.ptr(ss2),
               _lib.ptr(smooth), _lib.ptr(share_smooth), _lib.ptr(mask), bs, h, k, n1, nsh,
-              3 if fp8 else 2 if int8 else 0, ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs, _lib.ptr(out),
+              (3 if fp8 else 2 if int8 else 0) | (WEIGHT_LIST if separated else 0), ep_rank_size, ep_rank_id, moe_expert_num, quant_mode, global_bs, _lib.ptr(out),
               _lib.ptr(share_out), _lib.ptr(etn), device=x.device)
     return [out, share_out, etn]
 
