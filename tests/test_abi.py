@@ -164,3 +164,15 @@ def test_gmm_workspace_sizes(L):
     st, ws, ex, _ = _gmm1(L, m=1000, k=1024, n=512, dt=2, oq=2)
     L.camhipReleaseExecutor(ex)
     assert st == 0 and ws == ((1000 * 256 * 4 + 255) & ~255) + 1000 * (256 // 32) * 4   # h, then I/32 maxima per row
+
+
+def test_weight_pointer_tables_cached():
+    # separated fused_deep_moe weights go to the kernels as device arrays of per-expert pointers; the
+    # table for one set of pointers is built once and reused (host logic only: CPU tensors stand in)
+    import torch
+    from umdk_amd import ops
+    ts = [torch.zeros(4) for _ in range(3)]
+    t1 = ops._ptr_table(ts, "cpu")
+    assert t1.dtype == torch.int64 and t1.tolist() == [t.data_ptr() for t in ts]
+    assert ops._ptr_table(ts, "cpu") is t1
+    assert ops._ptr_table(ts[::-1], "cpu").tolist() == [t.data_ptr() for t in ts[::-1]]

@@ -337,18 +337,26 @@ def _per_expert(ws, L, what, coupled_dim):
 
 
 _PTR_TABLES = {}
+_PTR_PINNED = set()   # tables a captured graph may read: never freed
 
 
 def _ptr_table(ts, device):
     """Device array of the tensors' data pointers (int64), cached by the pointer values so that a
-    steady caller (and a captured graph) reuses one table."""
+    steady caller (and a captured graph) reuses one table.  A table used during graph capture is
+    kept for the life of the process; other tables are dropped when the cache fills."""
     key = (str(device),) + tuple(t.data_ptr() for t in ts)
     tab = _PTR_TABLES.get(key)
+    capturing = torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing()
     if tab is None:
-        if len(_PTR_TABLES) >= 64:
-            _PTR_TABLES.clear()
+        _check(not capturing, "fused_deep_moe: separated weights first seen inside graph capture; "
+               "run the call once before capturing (its pointer table is built eagerly)")
+        if len(_PTR_TABLES) >= 256:
+            for k in [k for k in _PTR_TABLES if k not in _PTR_PINNED]:
+                del _PTR_TABLES[k]
         tab = torch.tensor(key[1:], dtype=torch.int64).to(device)
         _PTR_TABLES[key] = tab
+    if capturing:
+        _PTR_PINNED.add(key)
     return tab
 
 
