@@ -231,25 +231,31 @@ def measured_peaks():
             "note": "2 GiB fp32 copy (read + write bytes) and fp32 sum over 2 GiB; 8192^3 GEMMs via the vendor library"}
 
 
-def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536)):
-    """fp8 GMM1+GMM2 at DeepSeek-V3 expert shapes (32 experts, H=7168, I=2048) for growing M."""
+def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536), dt="fp8"):
+    """fp8 (or int8 W8A8) GMM1+GMM2 at DeepSeek-V3 expert shapes (32 experts, H=7168, I=2048) for
+    growing M."""
     from umdk_amd import ops
     dev = torch.device("cuda:0")
     H, I, L = 7168, 2048, 32
-    w1, s1, w2, s2 = make_weights(L, H, I, "fp8", dev, seed)
+    w1, s1, w2, s2 = make_weights(L, H, I, dt, dev, seed)
+    oq = 3 if dt == "fp8" else 2
     out = []
     for M in ms:
         gl = torch.full((L,), M // L, dtype=torch.int64, device=dev)
-        xq = (torch.randn(M, H, device=dev) * 0.5).to(torch.float8_e4m3fn)
-        xs = torch.full((M, H // 128), 0.01, device=dev)
+        if dt == "fp8":
+            xq = (torch.randn(M, H, device=dev) * 0.5).to(torch.float8_e4m3fn)
+            xs = torch.full((M, H // 128), 0.01, device=dev)
+        else:
+            xq = torch.randint(-127, 128, (M, H), dtype=torch.int8, device=dev)
+            xs = torch.full((M,), 0.01, device=dev)
         for _ in range(warmup):
-            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, 3)
+            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, oq)
             ops.grouped_matmul(h, hs, gl, w2, s2)
         torch.cuda.synchronize()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record()
         for _ in range(steps):
-            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, 3)
+            h, hs = ops.grouped_matmul_swiglu(xq, xs, gl, w1, s1, oq)
         e[1].record()
         for _ in range(steps):
             ops.grouped_matmul(h, hs, gl, w2, s2)
@@ -259,7 +265,7 @@ def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536)):
         t2 = e[1].elapsed_time(e[2]) / steps
         f1, f2 = 2.0 * M * H * 2 * I, 2.0 * M * I * H
         out.append({"M": M, "gmm1_ms": t1, "gmm1_tflops": f1 / t1 / 1e9, "gmm2_ms": t2, "gmm2_tflops": f2 / t2 / 1e9,
-                    "frac_of_fp8_peak": (f1 + f2) / (t1 + t2) / 1e9 / FP8_PEAK_TFLOPS})
+                    "frac_of_peak": (f1 + f2) / (t1 + t2) / 1e9 / (FP8_PEAK_TFLOPS if dt == "fp8" else INT8_PEAK_TOPS)})
     return out
 
 
@@ -333,9 +339,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "4i8", "5", "5i8", "sweep", "peaks", "all"],
+    ap.add_argument("--config", default="default", choices=["default", "2", "3", "4", "4i8", "5", "5i8", "sweep", "sweepi8", "peaks", "all"],
                     help="default: the config-2 headline line plus brief config 3/4/5 results; 2: config 2 only; "
-                         "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; peaks: measured copy/read bandwidth and vendor GEMM rates; sweep: fp8 grouped-GEMM M-sweep; all: default + sweep")
+                         "3/4/5: only that config; 5i8: config 5 with int8 W8A8 weights; peaks: measured copy/read bandwidth and vendor GEMM rates; sweep: fp8 grouped-GEMM M-sweep; sweepi8: the same with int8 W8A8; all: default + sweep")
     ap.add_argument("--sweep-m", type=int, default=0, help="--config sweep: only this M")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run 20 device copies of 1 GiB (known bytes) to calibrate HBM counters")
@@ -364,13 +370,16 @@ def main():
     if args.config == "peaks":
         print(json.dumps({"config": "peaks", "result": measured_peaks()}))
         return
-    if args.config in ("3", "4", "4i8", "5", "5i8", "sweep"):
+    if args.config in ("3", "4", "4i8", "5", "5i8", "sweep", "sweepi8"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
              "4i8": lambda: cfg4(args.steps, args.warmup, "int8"),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed),
              "5i8": lambda: run_decode(max(args.steps, 1000), args.seed, "int8"),
              "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
-                                         (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536))
+                                         (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536)),
+             "sweepi8": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
+                                           (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536),
+                                           "int8"),
              }[args.config]()
         print(json.dumps({"config": args.config, "result": r}))
         return
