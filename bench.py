@@ -89,6 +89,51 @@ def cpu_baseline(T, H, E, K, seed):
                       f"CPUs ({model}); {dt * 1e3:.0f} ms/step"}
 
 
+def cpu_gemm_row_seconds(dt, H, I, seed, budget_s=5.0):
+    """Seconds per routed row of the C oracle's GMM1+SwiGLU+GMM2 (OpenMP over rows) at one expert's
+    shapes, timed on batches of rows until a bounded ~5 s sample is spent."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    rng = np.random.default_rng(seed)
+    rows = max(orc.num_threads(), 8)
+    cnt = np.array([rows], np.int64)
+    if dt == "fp8":
+        A = rng.integers(0, 0x7e, (rows, H), dtype=np.uint8)
+        As = np.full((rows, H // 128), 0.01, np.float32)
+        W1 = rng.integers(0, 0x7e, (1, 2 * I, H), dtype=np.uint8)
+        W1s = np.full((1, 2 * I // 128, H // 128), 0.01, np.float32)
+        W2 = rng.integers(0, 0x7e, (1, H, I), dtype=np.uint8)
+        W2s = np.full((1, H // 128, I // 128), 0.01, np.float32)
+        step = lambda: orc.gmm2_fp8(*orc.gmm1_swiglu_fp8(A, As, cnt, W1, W1s), cnt, W2, W2s)  # noqa: E731
+    else:
+        bf = lambda *sh: (torch.randn(*sh) * 0.05).bfloat16().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        A, W1, W2 = bf(rows, H), bf(1, 2 * I, H), bf(1, H, I)
+        step = lambda: orc.gmm2_bf16(orc.gmm1_swiglu_bf16(A, cnt, W1), cnt, W2)  # noqa: E731
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += rows
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_layer_baseline(cfg_cpu, dt, T, H, I, M, seed):
+    """CPU oracle time of one layer: route + layout + dispatch + combine at the config-2 shapes (the same
+    T, H, E, K as config 4; cfg_cpu is that measured step, None for config 3, whose bookkeeping is
+    < 1% of its GEMMs) + M rows of the oracle's expert GEMMs."""
+    from oracle import oracle as orc
+    per_row, n = cpu_gemm_row_seconds(dt, H, I, seed)
+    step = (T / cfg_cpu["value"]) if cfg_cpu else 0.0
+    t = step + M * per_row
+    return {"value": T / t, "unit": "tokens/s", "cores": orc.num_threads(), "kind": "port",
+            "sample": f"{n} rows of the C oracle's {dt} GMM1+SwiGLU+GMM2 at H={H}, I={I} "
+                      f"({per_row * 1e3:.2f} ms/row, OpenMP over rows) x M={M}"
+                      + (f" + the measured config-2 step ({step * 1e3:.0f} ms)" if cfg_cpu else "")
+                      + f": {t:.1f} s per layer"}
+
+
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, POP/s
@@ -475,6 +520,12 @@ def main():
         result["fp8_gemm_sweep"] = gemm_sweep(10, 3, args.seed)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(T, H, E, K, args.seed)
+        if args.config in ("default", "all"):
+            c4 = result["config4"]
+            c4["cpu_baseline"] = cpu_layer_baseline(result["cpu_baseline"], "fp8", 4096, 7168, 2048,
+                                                    c4["local_rows_M"], args.seed)
+            c3 = result["config3"]
+            c3["cpu_baseline"] = cpu_layer_baseline(None, "bf16", 8192, 4096, 14336, c3["local_rows_M"], args.seed)
     print(json.dumps(result))
 
 

@@ -385,10 +385,11 @@ ORC_API void orc_gmm1_swiglu_bf16(const uint16_t *A, const int64_t *cnt, int L, 
 {
     int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
     seg_offsets(cnt, L, off);
-    float *a = (float *)malloc(sizeof(float) * (size_t)H);
     for (int e = 0; e < L; ++e) {
         const uint16_t *W = W1 + (size_t)e * 2 * I * H;
+#pragma omp parallel for schedule(dynamic, 1)
         for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            float *a = (float *)malloc(sizeof(float) * (size_t)H);
             for (int h = 0; h < H; ++h)
                 a[h] = bf16_to_f32(A[(size_t)m * H + h]);
             for (int i = 0; i < I; ++i) {
@@ -400,9 +401,9 @@ ORC_API void orc_gmm1_swiglu_bf16(const uint16_t *A, const int64_t *cnt, int L, 
                 }
                 hout[(size_t)m * I + i] = f32_to_bf16(silu((float)g) * (float)u);
             }
+            free(a);
         }
     }
-    free(a);
     free(off);
 }
 
@@ -411,10 +412,11 @@ ORC_API void orc_gmm2_bf16(const uint16_t *Hin, const int64_t *cnt, int L, const
 {
     int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
     seg_offsets(cnt, L, off);
-    float *a = (float *)malloc(sizeof(float) * (size_t)I);
     for (int e = 0; e < L; ++e) {
         const uint16_t *W = W2 + (size_t)e * H * I;
+#pragma omp parallel for schedule(dynamic, 1)
         for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            float *a = (float *)malloc(sizeof(float) * (size_t)I);
             for (int i = 0; i < I; ++i)
                 a[i] = bf16_to_f32(Hin[(size_t)m * I + i]);
             for (int n = 0; n < H; ++n) {
@@ -424,9 +426,9 @@ ORC_API void orc_gmm2_bf16(const uint16_t *Hin, const int64_t *cnt, int L, const
                     s += (double)a[i] * (double)bf16_to_f32(w[i]);
                 out[(size_t)m * H + n] = f32_to_bf16((float)s);
             }
+            free(a);
         }
     }
-    free(a);
     free(off);
 }
 
@@ -438,14 +440,18 @@ ORC_API void orc_gmm1_swiglu_fp8(const uint8_t *A, const float *As, const int64_
                                  float *hs)
 {
     int kb = H / 128, nb2 = 2 * I / 128;
+    float lut[256];  /* e4m3 decode of every code */
+    for (int c = 0; c < 256; ++c)
+        lut[c] = e4m3_to_f32((uint8_t)c);
     int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
     seg_offsets(cnt, L, off);
-    double *a = (double *)malloc(sizeof(double) * (size_t)H);
-    float *hrow = (float *)malloc(sizeof(float) * (size_t)I);
     for (int e = 0; e < L; ++e) {
         const uint8_t *W = W1 + (size_t)e * 2 * I * H;
         const float *Ws = W1s + (size_t)e * nb2 * kb;
+#pragma omp parallel for schedule(dynamic, 1)
         for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            double *a = (double *)malloc(sizeof(double) * (size_t)H);
+            float *hrow = (float *)malloc(sizeof(float) * (size_t)I);
             for (int h = 0; h < H; ++h)
                 a[h] = (double)e4m3_to_f32(A[(size_t)m * H + h]) * (double)As[(size_t)m * kb + h / 128];
             for (int i = 0; i < I; ++i) {
@@ -453,8 +459,8 @@ ORC_API void orc_gmm1_swiglu_fp8(const uint8_t *A, const float *As, const int64_
                 const uint8_t *wg = W + (size_t)ng * H, *wu = W + (size_t)nu * H;
                 double g = 0.0, u = 0.0;
                 for (int h = 0; h < H; ++h) {
-                    g += a[h] * (double)e4m3_to_f32(wg[h]) * (double)Ws[(ng / 128) * kb + h / 128];
-                    u += a[h] * (double)e4m3_to_f32(wu[h]) * (double)Ws[(nu / 128) * kb + h / 128];
+                    g += a[h] * (double)lut[wg[h]] * (double)Ws[(ng / 128) * kb + h / 128];
+                    u += a[h] * (double)lut[wu[h]] * (double)Ws[(nu / 128) * kb + h / 128];
                 }
                 hrow[i] = silu((float)g) * (float)u;
             }
@@ -468,10 +474,10 @@ ORC_API void orc_gmm1_swiglu_fp8(const uint8_t *A, const float *As, const int64_
                     hq[(size_t)m * I + i] = f32_to_e4m3(hrow[i] * inv);
                 hs[(size_t)m * (I / 128) + b] = amax / 448.0f;
             }
+            free(hrow);
+            free(a);
         }
     }
-    free(hrow);
-    free(a);
     free(off);
 }
 
@@ -479,25 +485,29 @@ ORC_API void orc_gmm2_fp8(const uint8_t *Hq, const float *Hs, const int64_t *cnt
                           const uint8_t *W2, const float *W2s, int I, int H, uint16_t *out)
 {
     int kb = I / 128, nbk = H / 128;
+    float lut[256];  /* e4m3 decode of every code */
+    for (int c = 0; c < 256; ++c)
+        lut[c] = e4m3_to_f32((uint8_t)c);
     int64_t *off = (int64_t *)malloc(sizeof(int64_t) * (size_t)L);
     seg_offsets(cnt, L, off);
-    double *a = (double *)malloc(sizeof(double) * (size_t)I);
     for (int e = 0; e < L; ++e) {
         const uint8_t *W = W2 + (size_t)e * H * I;
         const float *Ws = W2s + (size_t)e * nbk * kb;
+#pragma omp parallel for schedule(dynamic, 1)
         for (int64_t m = off[e]; m < off[e] + cnt[e]; ++m) {
+            double *a = (double *)malloc(sizeof(double) * (size_t)I);
             for (int i = 0; i < I; ++i)
                 a[i] = (double)e4m3_to_f32(Hq[(size_t)m * I + i]) * (double)Hs[(size_t)m * kb + i / 128];
             for (int n = 0; n < H; ++n) {
                 const uint8_t *w = W + (size_t)n * I;
                 double s = 0.0;
                 for (int i = 0; i < I; ++i)
-                    s += a[i] * (double)e4m3_to_f32(w[i]) * (double)Ws[(n / 128) * kb + i / 128];
+                    s += a[i] * (double)lut[w[i]] * (double)Ws[(n / 128) * kb + i / 128];
                 out[(size_t)m * H + n] = f32_to_bf16((float)s);
             }
+            free(a);
         }
     }
-    free(a);
     free(off);
 }
 
