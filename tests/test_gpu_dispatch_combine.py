@@ -310,3 +310,31 @@ def test_dispatch_fp8_kmajor_scales_mode(ops):
     assert torch.equal(ex5[:N].view(torch.uint8), ex.view(torch.uint8))
     assert torch.equal(sc5[:, :N].t(), sc)
     assert torch.equal(ei5[:3 * N], eidx)
+
+
+def test_maximum_sizes_route_dispatch_combine(ops):
+    # the largest shapes the C ABI accepts at once: 65536 tokens x top-16 of 512 experts (1,048,576
+    # dispatched rows, 32-bit row offsets of 1 GiB fp8 output), with the smallest hidden size so the
+    # oracle stays quick; route, layout, fp8 dispatch and combine all bit-exact
+    T, H, E, K = 65536, 1024, 512, 16
+    print(f"max sizes T={T} H={H} E={E} K={K}", flush=True)
+    x, logits, bias = make_inputs(11, T, H, E, K, 0.5)
+    idx, w, ridx, rw = route_both(ops, logits, bias, K)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    idx_t = torch.from_numpy(ridx)
+    nte, sti, (ex, sc, eidx, rc, rtpe) = _dispatch(ops, x, idx_t, E, 3)
+    _, rnte, _, rsti = orc.dispatch_layout(ridx.astype(np.int64), E, 1)
+    so, rrc, rrtpe, tot = orc.notify_dispatch(rnte)
+    assert tot == T * K and ex.shape[0] == tot
+    assert np.array_equal(nte.cpu().numpy(), rnte) and np.array_equal(sti.cpu().numpy(), rsti)
+    assert np.array_equal(rc.cpu().numpy(), rrc)
+    rex, rsc, reidx = orc.dispatch(x.view(torch.int16).numpy().view(np.uint16), ridx, so, rsti, E, 3)
+    assert np.array_equal(eidx.cpu().numpy().reshape(-1, 3), reidx)
+    assert np.array_equal(ex.cpu().view(torch.uint8).numpy(), rex)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), rsc.view(np.uint32))
+    del ex, sc, rex, rsc
+    g = torch.Generator().manual_seed(12)
+    y = torch.randn(tot, H, generator=g).bfloat16()
+    out = ops.moe_combine_prefill(y.cuda(), idx_t.cuda(), torch.from_numpy(rw).cuda(), eidx, rc, "ep", 0, 1)
+    ref = orc.combine(bits(y), eidx.cpu().numpy(), ridx, rw, E)
+    assert np.array_equal(bits(out), ref)
