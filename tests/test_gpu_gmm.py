@@ -58,11 +58,18 @@ def dq_rows(q, s):
 
 # the first two cases take the 32-row tile (rows <= 48 per expert), the others the 128-row tile
 SMALL = [([3, 40, 0, 7], 1024, 256), ([1], 128 * 4, 128), ([5, 0, 300], 256, 256), ([17, 256, 255, 1, 0, 9], 512, 128)]
+# the ABI's largest group count (512 local experts), mostly empty: first with decode-sized rows (32-row
+# tile), then with one long segment that moves the launch onto the 8-wave kernel
+MAXL_A = [0] * 512
+MAXL_A[0], MAXL_A[255], MAXL_A[511] = 5, 70, 3
+MAXL_B = [0] * 512
+MAXL_B[3], MAXL_B[500], MAXL_B[511] = 25000, 40, 1
+SMALL += [(MAXL_A, 512, 128), (MAXL_B, 256, 128)]
 
 
 @pytest.mark.parametrize("counts,H,I", SMALL)
 def test_gmm_bf16_matches_oracle(ops, counts, H, I):
-    print(f"gmm bf16 counts={counts} H={H} I={I}", flush=True)
+    print(f"gmm bf16 groups={len(counts)} M={sum(counts)} H={H} I={I}", flush=True)
     g = torch.Generator().manual_seed(sum(counts) + H)
     L, M = len(counts), sum(counts)
     x = torch.randn(M + 3, H, generator=g).bfloat16()            # 3 spare rows past the groups
@@ -81,7 +88,7 @@ def test_gmm_bf16_matches_oracle(ops, counts, H, I):
 
 @pytest.mark.parametrize("counts,H,I", SMALL)
 def test_gmm_fp8_matches_oracle(ops, counts, H, I):
-    print(f"gmm fp8 counts={counts} H={H} I={I}", flush=True)
+    print(f"gmm fp8 groups={len(counts)} M={sum(counts)} H={H} I={I}", flush=True)
     g = torch.Generator().manual_seed(7 + sum(counts))
     L, M = len(counts), sum(counts)
     x = torch.randn(M + 3, H, generator=g)
