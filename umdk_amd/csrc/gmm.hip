@@ -446,9 +446,11 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         // 256-row fp8 tile (8 waves of 128 x 64): half the L2->LDS bytes per FLOP of the 128-row
         // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
         // W fragments of a k-step read once after the barrier, the A fragments streamed AHEAD rows
-        // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), and
-        // the next k-step's DMA issued during the first half of this k-step's MFMAs.  Tiles do not
-        // overlap: each starts with its own first DMA and drains at its end.
+        // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), the
+        // next k-step's A bands issued during the first half of this k-step's MFMAs and the W bands
+        // of the k-step after it from the middle on (a second barrier frees the W slot as soon as the
+        // fragments are in registers).  Tiles do not overlap: each starts with its own first DMA and
+        // drains at its end.
         static_assert(GSTAGES == 2, "two-stage ring");
         constexpr int AHEAD = 2;
         for (int tile = logical; tile < total; tile += G) {
@@ -462,13 +464,23 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                 pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
                 ps[j] = 0.0f;
             }
+            // the W bands of k-step 0, its A bands and scales, then the W bands of k-step 1
+#pragma unroll
+            for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
+                dma_one(c, 0, 0, q);
 #pragma unroll
             for (int q = 0; q < LOADS; ++q)
-                dma_one(c, 0, 0, q);
+                if (q < A_LOADS || q >= A_LOADS + B_LOADS)
+                    dma_one(c, 0, 0, q);
+#pragma unroll
+            for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
+                dma_one(c, min(1, nk - 1), 1, q);
             auto kloop = [&](auto act) {
                 for (int ks = 0; ks < nk; ++ks) {
-                    wait_vmcnt_lgkm0<0>();  // k-step ks has landed; this wave's reads of k-step ks-1 are done
-                    bar();                  // ... for every wave: slot (ks+1)%2 is free
+                    // k-step ks has landed (only the W bands of ks+1, issued last, may still be in flight);
+                    // this wave's reads of k-step ks-1 are done
+                    wait_vmcnt_lgkm0<B_LOADS>();
+                    bar();  // ... for every wave: the A/scale slot (ks+1)%2 is free
                     const uint8_t *st = smem + (ks & 1) * STAGE_BYTES;
                     const uint8_t *la = st + (wm * WM) * GKB;
                     const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
@@ -513,11 +525,23 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
                                 pend[j] = d;
                                 ps[j] = (SWIGLU && j >= JF / 2) ? sui : sgi;
                             }
+                            // the A bands and scales of k-step ks+1 over the first half of the MFMAs; at the
+                            // middle, when every wave has consumed its W fragments of ks, a barrier frees W
+                            // slot ks%2 and the W bands of ks+2 go into it: the W stream runs 1.5 k-steps
+                            // ahead in the same LDS.  All A/scale DMAs precede them (the wait above counts
+                            // on the W bands being the last B_LOADS issued).
                             const int n = i * JF + j;
-                            if (n < IF * JF / 2) {
+                            constexpr int HALF = IF * JF / 2, AS = LOADS - B_LOADS;
+                            if (n < HALF) {
 #pragma unroll
-                                for (int q = n * LOADS / (IF * JF / 2); q < (n + 1) * LOADS / (IF * JF / 2); ++q)
-                                    dma_one(c, kn, (ks + 1) & 1, q);
+                                for (int u = n * AS / HALF; u < (n + 1) * AS / HALF; ++u)
+                                    dma_one(c, kn, (ks + 1) & 1, u < A_LOADS ? u : u + B_LOADS);
+                            }
+                            if (n == HALF) {
+                                bar();
+#pragma unroll
+                                for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
+                                    dma_one(c, min(ks + 2, nk - 1), ks & 1, q);
                             }
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
                             __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
