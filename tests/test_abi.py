@@ -176,3 +176,27 @@ def test_weight_pointer_tables_cached():
     assert t1.dtype == torch.int64 and t1.tolist() == [t.data_ptr() for t in ts]
     assert ops._ptr_table(ts, "cpu") is t1
     assert ops._ptr_table(ts[::-1], "cpu").tolist() == [t.data_ptr() for t in ts[::-1]]
+
+
+def test_converted_weights_cached_per_source():
+    import torch
+    # a weight in the reference's contiguous [k, n] layout is transposed once per source tensor; the copy is
+    # reused while the source is unchanged, redone after an in-place update, and dropped with the source
+    from umdk_amd import ops
+    w = torch.arange(12, dtype=torch.float32).view(3, 4)       # logical [k=3, n=4]
+    a = ops._kmajor(w, 4, 3, "w")
+    assert a.is_contiguous() and torch.equal(a, w.t())
+    assert ops._kmajor(w, 4, 3, "w") is a
+    w.add_(1)
+    b = ops._kmajor(w, 4, 3, "w")
+    assert b is not a and torch.equal(b, w.t())
+    v = w.t().contiguous().t()                                  # k-contiguous storage underneath: no copy
+    assert ops._kmajor(v, 4, 3, "v").data_ptr() == v.data_ptr()
+    n = len(ops._CONVERTED)
+    del w, a, b
+    assert len(ops._CONVERTED) == n - 1
+    s = torch.ones(2, 3, dtype=torch.float64)
+    c = ops._contig(s, "s", torch.float32)
+    assert c.dtype == torch.float32 and ops._contig(s, "s", torch.float32) is c
+    f = torch.ones(2, 3)
+    assert ops._contig(f, "f", torch.float32) is f

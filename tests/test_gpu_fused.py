@@ -152,20 +152,21 @@ def test_fused_shared_expert_and_separated_weights(ops, dtype):
     out_s, sh_s, etn_s = call_fused(ops, d, E, separated=True)
     assert torch.equal(out_c.view(torch.int16), out_s.view(torch.int16)) and torch.equal(etn_c, etn_s)
     assert torch.equal(sh_c.view(torch.int16), sh_s.view(torch.int16))
-    # shared expert: dense SwiGLU FFN of every token, fp32 reference on dequantised operands
+    # shared expert: dense SwiGLU FFN of every token, checked against the oracle's chain for one expert that
+    # receives every token (dispatch with the fused op's quantiser, GMM1+SwiGLU with the fp8 requant of h, GMM2)
+    ids1 = np.zeros((bs, 1), np.int32)
+    sti1 = np.arange(bs, dtype=np.int32)[:, None]
+    so1 = np.zeros(1, np.int32)
+    cnt = np.array([bs], np.int64)
     if dtype == "bf16":
-        xd, w1d, w2d = d["x"].float(), d["sw1"].float(), d["sw2"].float()
+        ex, _, _ = orc.dispatch(b16(d["x"]), ids1, so1, sti1, 1, orc.QUANT_NONE)
+        h = orc.gmm1_swiglu_bf16(ex, cnt, b16(d["sw1"])[None])
+        ref = orc.gmm2_bf16(h, cnt, b16(d["sw2"])[None])
     else:
-        x = d["x"].float()
-        amax = x.view(bs, -1, 128).abs().amax(2).clamp(min=1e-4)
-        q = (x.view(bs, -1, 128) * (448.0 / amax).unsqueeze(2)).to(torch.float8_e4m3fn).float()
-        xd = (q * (amax / 448.0).unsqueeze(2)).view(bs, H)
-        w1d = (d["sw1"].float().view(2 * ish // 128, 128, H // 128, 128) * d["ss1"][:, None, :, None]).view(2 * ish, H)
-        w2d = (d["sw2"].float().view(H // 128, 128, ish // 128, 128) * d["ss2"][:, None, :, None]).view(H, ish)
-    gu = xd @ w1d.T
-    hh = gu[:, :ish] / (1 + torch.exp(-gu[:, :ish])) * gu[:, ish:]
-    ref = hh @ w2d.T
-    assert relerr(sh_c.float(), ref) < (2e-2 if dtype == "bf16" else 6e-2)
+        ex, xs, _ = orc.dispatch(b16(d["x"]), ids1, so1, sti1, 1, orc.QUANT_FP8)
+        hq, hs = orc.gmm1_swiglu_fp8(ex, xs, cnt, u8(d["sw1"])[None], d["ss1"].cpu().numpy()[None])
+        ref = orc.gmm2_fp8(hq, hs, cnt, u8(d["sw2"])[None], d["ss2"].cpu().numpy()[None])
+    assert relerr(sh_c.cpu().float(), orc.bf16_to_f32(ref)) < (2e-2 if dtype == "bf16" else 5e-2)
 
 
 def test_fused_graph_capture_replays(ops):
@@ -193,20 +194,27 @@ def test_fused_graph_capture_replays(ops):
         del junk
 
 
+@pytest.mark.parametrize("layout", ["kmajor_view", "reference_contiguous"])
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-def test_fused_separated_allocations_in_place(ops, dtype):
+def test_fused_separated_allocations_in_place(ops, dtype, layout):
     # dynamic-EPLB weights (test_fused_deep_moe.py:256-269): one allocation per expert, made in a
-    # scrambled order, weights and scales both as lists.  The op reads them in place through device
-    # pointer tables: bit-identical to the coupled call, no stacked copy of the weights, and a graph
-    # captured on the lists replays correctly.
+    # scrambled order, weights and scales both as lists.  "kmajor_view": transposed views of k-contiguous
+    # storage, read in place through device pointer tables (no copy at all).  "reference_contiguous": the
+    # reference's own contiguous [k, n] per-expert tensors (what its clone() produces), converted once and
+    # cached on the source tensors, so later calls and a captured graph make no copy.  Both are
+    # bit-identical to the coupled call and a graph captured on the lists replays correctly.
     bs, H, I, E, K = 128, 7168, 256, 32, 8
     d = make(7, bs, H, I, E, K, dtype)
     ref, _, etn_ref = call_fused(ops, d, E)
     order = torch.randperm(E, generator=torch.Generator().manual_seed(1)).tolist()
     g1, g2, s1, s2 = [None] * E, [None] * E, [None] * E, [None] * E
     for e in order:
-        g1[e] = d["w1"][e].clone().transpose(0, 1)       # logical [H, 2I] over k-contiguous storage
-        g2[e] = d["w2"][e].clone().transpose(0, 1)
+        if layout == "kmajor_view":
+            g1[e] = d["w1"][e].clone().transpose(0, 1)       # logical [H, 2I] over k-contiguous storage
+            g2[e] = d["w2"][e].clone().transpose(0, 1)
+        else:
+            g1[e] = d["w1"][e].transpose(0, 1).contiguous()  # logical [H, 2I], contiguous
+            g2[e] = d["w2"][e].transpose(0, 1).contiguous()
         if dtype == "fp8":
             s1[e] = d["s1"][e].clone()
             s2[e] = d["s2"][e].clone()
@@ -216,6 +224,9 @@ def test_fused_separated_allocations_in_place(ops, dtype):
                                       None, None, None, "ep", 1, 0, E, 0, 0)
     torch.cuda.synchronize()
     wbytes = sum(t.numel() * t.element_size() for t in g1 + g2)
+    if layout == "reference_contiguous":
+        call()                       # the one conversion per source tensor
+        torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
     out, _, etn = call()
@@ -238,6 +249,12 @@ def test_fused_separated_allocations_in_place(ops, dtype):
         assert torch.equal(gout.view(torch.int16), ref.view(torch.int16)), f"replay {r}"
         assert torch.equal(getn, etn_ref)
         del junk
+    if layout == "reference_contiguous":
+        # an in-place update of a source tensor (a new expert placement) is picked up by the next eager call
+        g1[0].zero_()
+        out2, _, _ = call()
+        torch.cuda.synchronize()
+        assert not torch.equal(out2.view(torch.int16), ref.view(torch.int16))
 
 
 def test_fused_rejects_bad_weight_lists(ops):

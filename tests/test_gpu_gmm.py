@@ -210,6 +210,12 @@ def test_gmm_long_segments_take_256_row_tile(ops, dtype):
     _ragged_vs_torch(ops, [700, 0, 1100, 520], 2048, 512, dtype, 5, 21)
 
 
+def test_gmm_fp8_256_row_tile_long_reductions(ops):
+    # the 256-row fp8 k-loop runs for reductions of >= 32 k-steps: H = I = 4096 sends both GMM1 (SwiGLU
+    # epilogue) and GMM2 (plain bf16 epilogue) of the >= 384-row experts through it
+    _ragged_vs_torch(ops, [700, 0, 1100, 520], 4096, 4096, "fp8", 5, 26)
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
 def test_gmm_short_segments_in_large_capacity_take_128_row_tile(ops, dtype):
     # a 4096-row capacity (prefill-sized) holding 45 rows: the device picks the 128-row tile over the 256-row one

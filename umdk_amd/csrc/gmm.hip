@@ -41,6 +41,7 @@
 //     groups of 8 M-tiles x all N-tiles (M fastest), remapped so that the
 //     blocks of one XCD take consecutive tiles: they share A and W tiles in
 //     that XCD's L2.
+#include <atomic>
 #include <type_traits>
 
 #include "cam_device.h"
@@ -884,26 +885,43 @@ static_assert(lds_bytes<32>() <= 163840 && lds_bytes<128>() <= 163840 && lds_byt
               "LDS budget of a gfx950 workgroup");
 
 
-static int g_num_cus = 0;
+// Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
+// Both are cached per device in atomics, so concurrent first calls and several GPUs are safe (a
+// racing first call only repeats the idempotent query or attribute set).
+constexpr int G_MAX_DEVICES = 64;
 
-static int num_cus()
+static int current_device()
 {
-    if (g_num_cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        g_num_cus = n;
-    }
-    return g_num_cus;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+        dev = 0;
+    return dev;
 }
 
-template <typename K> static hipError_t set_lds(K kernel, size_t lds, bool &done)
+static int num_cus(int dev)
 {
-    if (done)
+    static std::atomic<int> cache[G_MAX_DEVICES];
+    if (dev < G_MAX_DEVICES) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0)
+            return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    if (dev < G_MAX_DEVICES)
+        cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// one flag per device and kernel instantiation (the caller passes its own static array)
+template <typename K> static hipError_t set_lds(K kernel, size_t lds, int dev, std::atomic<bool> *done)
+{
+    if (dev < G_MAX_DEVICES && done[dev].load(std::memory_order_acquire))
         return hipSuccess;
     hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    done = e == hipSuccess;
+    if (e == hipSuccess && dev < G_MAX_DEVICES)
+        done[dev].store(true, std::memory_order_release);
     return e;
 }
 
@@ -913,20 +931,21 @@ template <typename K> static hipError_t set_lds(K kernel, size_t lds, bool &done
 // segments when most rows are routed elsewhere).  One launch, no host synchronisation.
 template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s)
 {
-    const int grid = (num_cus() + 7) / 8 * 8;
+    const int dev = current_device();
+    const int grid = (num_cus(dev) + 7) / 8 * 8;
     if (a.M <= 48 * a.L) {
-        static bool done = false;
+        static std::atomic<bool> done[G_MAX_DEVICES];
         const size_t lds = lds_bytes<32>();
-        hipError_t e = set_lds(gmm_kernel_small<DT, EPI>, lds, done);
+        hipError_t e = set_lds(gmm_kernel_small<DT, EPI>, lds, dev, done);
         if (e != hipSuccess)
             return e;
         hipLaunchKernelGGL((gmm_kernel_small<DT, EPI>), dim3(grid), dim3(256), lds, s, a);
         return hipGetLastError();
     }
     a.allow256 = a.M >= G_HEAVY_ROWS;  // some expert may reach the 256-row tile class
-    static bool done = false;
+    static std::atomic<bool> done[G_MAX_DEVICES];
     const size_t lds = lds_bytes<128>() > lds_bytes<256>() ? lds_bytes<128>() : lds_bytes<256>();
-    hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, done);
+    hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, dev, done);
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL((gmm_kernel_big<DT, EPI>), dim3(grid), dim3(512), lds, s, a);

@@ -18,6 +18,8 @@ Differences, all documented in the op docstrings:
   * moe_route (routing) and grouped expert GEMM ops are additions with no
     reference counterpart.
 """
+import weakref
+
 import torch
 
 from . import _lib
@@ -285,14 +287,50 @@ def prepack_weight(w_lkn):
     return w_lkn.transpose(1, 2).contiguous()
 
 
+_CONVERTED = {}
+
+
+def _converted(src, tag, make):
+    """A layout or dtype conversion of a weight-like input, made once per source tensor.
+
+    The result is cached on the source tensor object and its version counter, so a caller that passes
+    the same weights on every step (the reference's dynamic-EPLB lists, test_fused_deep_moe.py:256-269)
+    pays the copy once, keeps one stable device address (a captured graph reads it) and re-converts only
+    after the source is modified in place.  The entry is dropped when the source is freed.  A conversion
+    first needed inside graph capture is refused: the copy would land in the graph's private pool."""
+    key = (id(src), tag)
+    ent = _CONVERTED.get(key)
+    if ent is not None and ent[0]() is src and ent[1] == src._version:
+        return ent[2]
+    _check(not (src.is_cuda and torch.cuda.is_current_stream_capturing()),
+           f"fused_deep_moe: {tag} needs a converted copy (layout or dtype) that cannot be made inside graph "
+           "capture; run the call once eagerly before capturing, or pass the kernels' own layout")
+    out = make()
+
+    def _drop(_ref, key=key):
+        _CONVERTED.pop(key, None)
+
+    _CONVERTED[key] = (weakref.ref(src, _drop), src._version, out)
+    return out
+
+
+def _contig(t, tag, dtype=None):
+    """t as a contiguous tensor of `dtype` (default: its own), converted once per source (see _converted)."""
+    dtype = t.dtype if dtype is None else dtype
+    if t.dtype == dtype and t.is_contiguous():
+        return t
+    return _converted(t, tag, lambda: t.to(dtype).contiguous())
+
+
 def _kmajor(w, n, k, what):
-    """A weight given in the reference's logical [..., k, n] shape -> storage with k contiguous
-    ([..., n, k]).  A transposed view of such storage is used as is; a contiguous [..., k, n]
-    tensor is transposed once (a copy)."""
-    if tuple(w.shape[-2:]) == (k, n) and w.stride(-2) == 1 and w.stride(-1) == k:
-        return w.transpose(-1, -2)          # already k-contiguous underneath: no copy
+    """A weight given in the reference's logical [..., k, n] shape -> contiguous storage with k contiguous
+    ([..., n, k]).  A transposed view of such storage is used as is; a contiguous [..., k, n] tensor is
+    transposed once per source tensor (a cached copy, see _converted)."""
     if tuple(w.shape[-2:]) == (k, n):
-        return w.transpose(-1, -2).contiguous()
+        t = w.transpose(-1, -2)
+        if t.is_contiguous():
+            return t                       # already k-contiguous underneath: no copy
+        return _converted(w, what, lambda: t.contiguous())
     raise RuntimeError(f"fused_deep_moe: {what} must have logical shape [..., {k}, {n}], got {tuple(w.shape)}")
 
 
@@ -303,7 +341,7 @@ def _is_coupled(ws):
 def _coupled(ws, L, n, k, what):
     w = _kmajor(ws[0], n, k, what)
     _check(tuple(w.shape) == (L, n, k), f"fused_deep_moe: {what} shape mismatch")
-    return w.contiguous()
+    return w
 
 
 def _scales(ss, L, n, k, what):
@@ -313,7 +351,7 @@ def _scales(ss, L, n, k, what):
     s = ss[0]
     _check(s.dim() == 3 and s.dtype == torch.float32 and tuple(s.shape) == (L, n // 128, k // 128),
            f"fused_deep_moe: {what} must be float32 [{L}, {n // 128}, {k // 128}] (128x128 block scales)")
-    return s.contiguous()
+    return _contig(s, what)
 
 
 def _channel_scales(ss, L, n, what):
@@ -322,7 +360,7 @@ def _channel_scales(ss, L, n, what):
     _check(bool(ss) and ss[0] is not None, f"fused_deep_moe: int8 weights need {what}")
     s = ss[0]
     _check(s.dim() == 2 and tuple(s.shape) == (L, n), f"fused_deep_moe: {what} must be [{L}, {n}] per-channel scales")
-    return s.to(torch.float32).contiguous()
+    return _contig(s, what, torch.float32)
 
 
 def _per_expert(ws, L, what, coupled_dim):
@@ -357,6 +395,10 @@ def _ptr_table(ts, device):
         _PTR_TABLES[key] = tab
     if capturing:
         _PTR_PINNED.add(key)
+    elif tab.is_cuda:
+        # a cached table may be reused from another stream: the allocator must not hand its memory out
+        # again (after the cache drops it) before that stream's reads are done
+        tab.record_stream(torch.cuda.current_stream(tab.device))
     return tab
 
 
@@ -374,12 +416,12 @@ def _separated(ws, ss, L, n, k, fp8, int8, what, device):
         sname = what + "_scale"
         se = _per_expert(ss, L, sname, 3 if fp8 else 2)
         if fp8:
-            se = [t.contiguous() for t in se]
+            se = [_contig(t, sname) for t in se]
             for t in se:
                 _check(t.dtype == torch.float32 and tuple(t.shape) == (n // 128, k // 128),
                        f"fused_deep_moe: each {sname} must be float32 [{n // 128}, {k // 128}]")
         else:
-            se = [t.to(torch.float32).contiguous().view(-1) for t in se]
+            se = [_contig(t, sname, torch.float32).view(-1) for t in se]
             for t in se:
                 _check(t.numel() == n, f"fused_deep_moe: each {sname} must have {n} per-channel scales")
         keep += se
@@ -444,29 +486,29 @@ def fused_deep_moe(x, expert_ids, gmm1_weight, gmm1_weight_scale, gmm2_weight, g
         _check(int8, "fused_deep_moe: expert_smooth_scales need int8 weights")
         _check(tuple(expert_smooth_scales.shape) == (moe_expert_num, h),
                f"fused_deep_moe: expert_smooth_scales must be [{moe_expert_num}, {h}]")
-        smooth = expert_smooth_scales.to(torch.float32).contiguous()
+        smooth = _contig(expert_smooth_scales, "expert_smooth_scales", torch.float32)
     if share_smooth_scales is not None and share_gmm1_weight is not None:   # ignored without a shared expert
         _check(int8, "fused_deep_moe: share_smooth_scales need int8 weights")
         _check(share_smooth_scales.numel() == h, f"fused_deep_moe: share_smooth_scales must have {h} elements")
-        share_smooth = share_smooth_scales.to(torch.float32).contiguous().view(h)
+        share_smooth = _contig(share_smooth_scales, "share_smooth_scales", torch.float32).view(h)
     shared = share_gmm1_weight is not None
     sw1 = sw2 = ss1 = ss2 = None
     nsh = 0
     if shared:
         _check(share_gmm2_weight is not None, "fused_deep_moe: share_gmm2_weight missing")
         nsh = share_gmm1_weight.shape[-1]
-        sw1 = _kmajor(share_gmm1_weight, nsh, h, "share_gmm1_weight").contiguous()
-        sw2 = _kmajor(share_gmm2_weight, h, nsh // 2, "share_gmm2_weight").contiguous()
+        sw1 = _kmajor(share_gmm1_weight, nsh, h, "share_gmm1_weight")
+        sw2 = _kmajor(share_gmm2_weight, h, nsh // 2, "share_gmm2_weight")
         if fp8:
-            ss1 = share_gmm1_weight_scale.contiguous()
-            ss2 = share_gmm2_weight_scale.contiguous()
+            ss1 = _contig(share_gmm1_weight_scale, "share_gmm1_weight_scale")
+            ss2 = _contig(share_gmm2_weight_scale, "share_gmm2_weight_scale")
         elif int8:
             _check(share_gmm1_weight_scale is not None and share_gmm2_weight_scale is not None,
                    "fused_deep_moe: int8 shared expert needs share_gmm1/2_weight_scale")
             _check(share_gmm1_weight_scale.numel() == nsh and share_gmm2_weight_scale.numel() == h,
                    f"fused_deep_moe: int8 shared scales must be [{nsh}] and [{h}]")
-            ss1 = share_gmm1_weight_scale.to(torch.float32).contiguous().view(nsh)
-            ss2 = share_gmm2_weight_scale.to(torch.float32).contiguous().view(h)
+            ss1 = _contig(share_gmm1_weight_scale, "share_gmm1_weight_scale", torch.float32).view(nsh)
+            ss2 = _contig(share_gmm2_weight_scale, "share_gmm2_weight_scale", torch.float32).view(h)
     ids = expert_ids if expert_ids.dtype == torch.int32 else expert_ids.to(torch.int32)
     ids = ids.contiguous()
     es = expert_scales if expert_scales.dtype == torch.float32 else expert_scales.to(torch.float32)
