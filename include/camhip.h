@@ -161,6 +161,22 @@ CAMHIP_API camhipStatus camhipMoeCombineNormalGetWorkspaceSize(
 CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                void *stream);
 
+/* Allocation-free combine.  No reference counterpart: for callers that cannot allocate or pass a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same arguments and results as camhipMoeCombineNormalGetWorkspaceSize + camhipMoeCombineNormal in
+ * one call; the row map lives in a static per-device scratch array of the library (1 MiB + 256 B per
+ * GPU, held until the process ends), so numTokens * numTopk must not exceed
+ * CAMHIP_COMBINE_NOALLOC_MAX_SLOTS (CAMHIP_ERROR_INVALID_PARAM otherwise).  Every call on a GPU shares
+ * that scratch: calls that overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller.  No hipMalloc, hipFree or allocating library call is made. */
+#define CAMHIP_COMBINE_NOALLOC_MAX_SLOTS (1L << 18)
+CAMHIP_API camhipStatus camhipMoeCombineNormalNoAlloc(const uint16_t *recvX, const int32_t *tokenSrcInfo,
+                                                      int64_t numRecvRows, const int32_t *epRecvCounts,
+                                                      const float *recvTopkWeights, int64_t numTokens,
+                                                      int64_t numTopk, int64_t hidden, int64_t epWorldSize,
+                                                      int64_t epRankId, int64_t moeExpertNum, uint16_t *out,
+                                                      int32_t *sendCostStats, void *stream);
+
 /* ------------------------------------------------------------------ grouped expert GEMMs
  * The GMM1 / SwiGLU / GMM2 stages of fused_deep_moe as standalone calls
  * (fused_deep_moe.h:56-238; kernels

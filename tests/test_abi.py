@@ -200,3 +200,11 @@ def test_converted_weights_cached_per_source():
     assert c.dtype == torch.float32 and ops._contig(s, "s", torch.float32) is c
     f = torch.ones(2, 3)
     assert ops._contig(f, "f", torch.float32) is f
+
+
+def test_combine_noalloc_rejects_beyond_its_scratch(L):
+    # 65536 tokens x top-8 = 524288 row slots: past the static scratch (262144 slots); rejected before any launch
+    st = L.camhipMoeCombineNormalNoAlloc(P, P, 8, None, P, 65536, 8, 1024, 1, 0, 8, P, None, None)
+    assert st == 161001 and "static scratch" in L.camhipGetLastErrorMsg().decode()
+    st = L.camhipMoeCombineNormalNoAlloc(P, P, 8, None, P, 4, 2, 1000, 1, 0, 8, P, None, None)
+    assert st == 161001 and "hidden" in L.camhipGetLastErrorMsg().decode()

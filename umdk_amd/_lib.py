@@ -55,6 +55,10 @@ def lib():
             g = getattr(L, name)
             g.restype = ctypes.c_int
             g.argtypes = [_P, ctypes.c_uint64, _P, _P]
+        # the allocation-free combine: the combine's GetWorkspaceSize arguments without the workspace
+        # outputs, then the stream
+        L.camhipMoeCombineNormalNoAlloc.restype = ctypes.c_int
+        L.camhipMoeCombineNormalNoAlloc.argtypes = [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P]
         _lib = L
     return _lib
 

@@ -15,6 +15,8 @@
 #include "gmm.h"
 #include "launchers.h"
 
+static_assert(CAMHIP_COMBINE_NOALLOC_MAX_SLOTS == cam::COMBINE_NOALLOC_MAX_SLOTS, "scratch size of the header");
+
 struct camhipExecutor {
     uint64_t workspace_bytes = 0;
     std::function<hipError_t(void *ws, hipStream_t s)> launch;
@@ -297,12 +299,9 @@ camhipStatus camhipMoeDispatchNormal(void *workspace, uint64_t workspaceSize, ca
 }
 
 // ---------------------------------------------------------------- combine
-camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const int32_t *tokenSrcInfo,
-                                                    int64_t numRecvRows, const int32_t *epRecvCounts,
-                                                    const float *recvTopkWeights, int64_t numTokens, int64_t numTopk,
-                                                    int64_t hidden, int64_t epWorldSize, int64_t epRankId,
-                                                    int64_t moeExpertNum, uint16_t *out, int32_t *sendCostStats,
-                                                    uint64_t *workspaceSize, camhipExecutor **executor)
+static camhipStatus check_combine(const uint16_t *recvX, const int32_t *tokenSrcInfo, int64_t numRecvRows,
+                                  const float *recvTopkWeights, int64_t numTokens, int64_t numTopk, int64_t hidden,
+                                  int64_t epWorldSize, int64_t epRankId, int64_t moeExpertNum, uint16_t *out)
 {
     CHECK_PARAM(epWorldSize == 1 && epRankId == 0,
                 "moe_combine: this build runs one EP rank per GPU (epWorldSize %lld, epRankId %lld; need 1, 0)",
@@ -326,6 +325,20 @@ camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const
             CHECK_PTR(tokenSrcInfo);
         }
     }
+    return CAMHIP_SUCCESS;
+}
+
+camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const int32_t *tokenSrcInfo,
+                                                    int64_t numRecvRows, const int32_t *epRecvCounts,
+                                                    const float *recvTopkWeights, int64_t numTokens, int64_t numTopk,
+                                                    int64_t hidden, int64_t epWorldSize, int64_t epRankId,
+                                                    int64_t moeExpertNum, uint16_t *out, int32_t *sendCostStats,
+                                                    uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    camhipStatus st = check_combine(recvX, tokenSrcInfo, numRecvRows, recvTopkWeights, numTokens, numTopk, hidden,
+                                    epWorldSize, epRankId, moeExpertNum, out);
+    if (st != CAMHIP_SUCCESS)
+        return st;
     const int N = (int)numRecvRows, T = (int)numTokens, K = (int)numTopk, H = (int)hidden;
     const int32_t *last = epRecvCounts ? epRecvCounts + (moeExpertNum - 1) : nullptr;
     // workspace: the row map [T*K] int32, then (diagnose output requested) the phase's start stamp
@@ -353,6 +366,28 @@ camhipStatus camhipMoeCombineNormalGetWorkspaceSize(const uint16_t *recvX, const
 camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
 {
     return run_executor("moe_combine", workspace, workspaceSize, executor, stream);
+}
+
+camhipStatus camhipMoeCombineNormalNoAlloc(const uint16_t *recvX, const int32_t *tokenSrcInfo, int64_t numRecvRows,
+                                           const int32_t *epRecvCounts, const float *recvTopkWeights, int64_t numTokens,
+                                           int64_t numTopk, int64_t hidden, int64_t epWorldSize, int64_t epRankId,
+                                           int64_t moeExpertNum, uint16_t *out, int32_t *sendCostStats, void *stream)
+{
+    camhipStatus st = check_combine(recvX, tokenSrcInfo, numRecvRows, recvTopkWeights, numTokens, numTopk, hidden,
+                                    epWorldSize, epRankId, moeExpertNum, out);
+    if (st != CAMHIP_SUCCESS)
+        return st;
+    CHECK_PARAM(numTokens * numTopk <= CAMHIP_COMBINE_NOALLOC_MAX_SLOTS,
+                "moe_combine_noalloc: numTokens * numTopk = %lld exceeds the static scratch of %lld row slots",
+                (long long)(numTokens * numTopk), (long long)CAMHIP_COMBINE_NOALLOC_MAX_SLOTS);
+    const int32_t *last = epRecvCounts ? epRecvCounts + (moeExpertNum - 1) : nullptr;
+    hipError_t e = cam::launch_combine_noalloc(recvX, tokenSrcInfo, (int)numRecvRows, last, recvTopkWeights,
+                                               (int)numTokens, (int)numTopk, (int)hidden, out, sendCostStats,
+                                               (int)epRankId, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(CAMHIP_ERROR_RUNTIME, "moe_combine_noalloc: launch failed: %s", hipGetErrorString(e));
+    g_last_error.clear();
+    return CAMHIP_SUCCESS;
 }
 
 // ---------------------------------------------------------------- grouped GEMMs

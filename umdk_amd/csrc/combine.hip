@@ -14,6 +14,9 @@
 // 0 <= r < rows and expand_idx[r] names (t,k) back, so stale workspace
 // contents can never select a row; such slots are skipped, as the fused
 // combine skips expert ids < 0.
+#include <atomic>
+#include <mutex>
+
 #include "cam_device.h"
 #include "launchers.h"
 
@@ -143,6 +146,70 @@ hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, c
                        dim3(COMB_WAVES * 64), 0, s, y, expand_idx, N, recv_count_last, topk_w, T, K, H, nchunk, out,
                        inv_ws);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- allocation-free combine
+// Scratch of the allocation-free entry point: the row map (T*K int32, at most
+// COMBINE_NOALLOC_MAX_SLOTS) and, past it, the diagnose output's 8-byte start stamp.  One copy
+// per GPU, held until the process ends; every call on a GPU shares it, so calls that overlap on
+// one GPU race.  Nothing in it needs clearing: the gather validates every map entry against
+// expand_idx, and the stamp is written before it is read.
+constexpr size_t NOALLOC_MAP_BYTES = sizeof(int32_t) * (size_t)COMBINE_NOALLOC_MAX_SLOTS;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_MAP_BYTES + 256];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<void *> g_scratch[NOALLOC_MAX_DEVICES];
+std::mutex g_scratch_mu;
+}  // namespace
+
+// Device address of `scratch` on the current device.  Host code never uses the array's name as
+// an address (on the host it is only a stand-in for the symbol): it asks the runtime once per
+// device, with that device current, and keeps the answer.
+hipError_t combine_noalloc_scratch(void **ptr)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return hipErrorInvalidDevice;
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess)
+                return e;
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *ptr = p;
+    return hipSuccess;
+}
+
+hipError_t launch_combine_noalloc(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                                  const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *cost_stats,
+                                  int stats_idx, hipStream_t s)
+{
+    if ((long)T * K > COMBINE_NOALLOC_MAX_SLOTS)
+        return hipErrorInvalidValue;
+    void *base = nullptr;
+    hipError_t e = combine_noalloc_scratch(&base);
+    if (e != hipSuccess)
+        return e;
+    int32_t *inv = (int32_t *)base;
+    uint64_t *stamp = (uint64_t *)((uint8_t *)base + NOALLOC_MAP_BYTES);
+    if (cost_stats) {
+        e = launch_phase_begin(stamp, s);
+        if (e != hipSuccess)
+            return e;
+    }
+    e = launch_combine(y, expand_idx, N, recv_count_last, topk_w, T, K, H, out, inv, s);
+    if (e != hipSuccess || !cost_stats)
+        return e;
+    return launch_phase_end(stamp, cost_stats, stats_idx, s);
 }
 
 }  // namespace cam

@@ -65,5 +65,11 @@ hipError_t launch_fill_i64(int64_t *p, int64_t v, long n, hipStream_t s);
 hipError_t launch_combine(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
                           const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *inv_ws,
                           hipStream_t s);
+// the same combine with its row map (and diagnose stamp) in the library's static per-device scratch:
+// no workspace, no allocation; T*K <= COMBINE_NOALLOC_MAX_SLOTS
+constexpr long COMBINE_NOALLOC_MAX_SLOTS = 1L << 18;
+hipError_t launch_combine_noalloc(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
+                                  const float *topk_w, int T, int K, int H, uint16_t *out, int32_t *cost_stats,
+                                  int stats_idx, hipStream_t s);
 
 }  // namespace cam
