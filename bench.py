@@ -119,6 +119,41 @@ def cpu_gemm_row_seconds(dt, H, I, seed, budget_s=5.0):
     return (time.perf_counter() - t0) / n, n
 
 
+def cpu_decode_baseline(x, logits, w1, s1, w2, s2, K, L, budget_s=10.0):
+    """The C oracle's whole decode step on the config-5 inputs themselves: route over all experts, layout and
+    count exchange over the L local experts, fp8 dispatch, GMM1 + SwiGLU + fp8 requant, GMM2, combine;
+    repeated for a bounded ~10 s sample."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    T = x.shape[0]
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    lg = logits.cpu().numpy()
+    u8 = lambda t: t.cpu().contiguous().view(torch.uint8).numpy()  # noqa: E731
+    hw1, hw2, hs1, hs2 = u8(w1), u8(w2), s1.cpu().numpy(), s2.cpu().numpy()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        idx, w = orc.route(lg, None, K)
+        rid = np.where(idx < L, idx, -1).astype(np.int32)
+        _, nte, _, sti = orc.dispatch_layout(rid.astype(np.int64), L, 1)
+        so, _, _, _ = orc.notify_dispatch(nte)
+        ex, xs, eidx = orc.dispatch(xb, rid, so, sti, L, orc.QUANT_FP8)
+        cnt = nte.astype(np.int64)
+        hq, hs = orc.gmm1_swiglu_fp8(ex, xs, cnt, hw1, hs1)
+        y = orc.gmm2_fp8(hq, hs, cnt, hw2, hs2)
+        orc.combine(y, eidx, rid, w, L)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    threads = orc.num_threads()
+    return {"value": dt * 1e6, "unit": "us per step (lower is better)", "tokens_per_s": T / dt, "cores": threads,
+            "kind": "port",
+            "sample": f"the config-5 step on the same inputs x{reps} through the C oracle (route, layout, fp8 "
+                      f"dispatch, GMM1+SwiGLU, GMM2, combine; {int(cnt.sum())} local rows), {threads} OpenMP "
+                      f"threads; {dt * 1e3:.1f} ms/step"}
+
+
 def cpu_layer_baseline(cfg_cpu, dt, T, H, I, M, seed):
     """CPU oracle time of one layer: route + layout + dispatch + combine at the config-2 shapes (the same
     T, H, E, K as config 4; cfg_cpu is that measured step, None for config 3, whose bookkeeping is
@@ -314,7 +349,7 @@ def gemm_sweep(steps, warmup, seed, ms=(4096, 8192, 16384, 32768, 65536), dt="fp
     return out
 
 
-def run_decode(steps, seed, dtype="fp8"):
+def run_decode(steps, seed, dtype="fp8", cpu=False):
     """Config 5: decode step (T=128, H=7168, route over 256 experts, 32 local experts, I=2048, fp8)
     = route + fused_deep_moe captured in one HIP graph; p50/p99 of single-replay times.  dtype "int8"
     runs the same step with the reference's int8 W8A8 weights (per-channel scales)."""
@@ -369,12 +404,16 @@ def run_decode(steps, seed, dtype="fp8"):
     touched = int((counts > 0).sum())
     wbytes = touched * 3 * H * I   # 1-byte W1 (2I x H) + W2 (H x I) of touched experts
     p50 = float(np.percentile(times, 50))
-    return {"workload": f"config5: decode step, route + fused_deep_moe in one HIP graph, {dtype}", "tokens": T,
+    cpu_base = cpu_decode_baseline(x, logits, w1, s1, w2, s2, K, L) if cpu and dtype == "fp8" else None
+    res = {"workload": f"config5: decode step, route + fused_deep_moe in one HIP graph, {dtype}", "tokens": T,
             "hidden": H, "experts_routed": E, "local_experts": L, "topk": K, "intermediate": I,
             "replays": steps, "p50_us": p50, "p99_us": float(np.percentile(times, 99)),
             "mean_us": float(times.mean()), "local_rows": int(counts.sum()), "experts_touched": touched,
             "weight_bytes_touched": wbytes, "weight_GBps_at_p50": wbytes / (p50 * 1e-6) / 1e9,
             "hbm_roofline_frac": (wbytes / (HBM_PEAK_GBPS * 1e9)) / (p50 * 1e-6)}
+    if cpu_base:
+        res["cpu_baseline"] = cpu_base
+    return res
 
 
 def main():
@@ -418,7 +457,7 @@ def main():
     if args.config in ("3", "4", "4i8", "5", "5i8", "sweep", "sweepi8"):
         r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
              "4i8": lambda: cfg4(args.steps, args.warmup, "int8"),
-             "5": lambda: run_decode(max(args.steps, 1000), args.seed),
+             "5": lambda: run_decode(max(args.steps, 1000), args.seed, cpu=not args.no_cpu),
              "5i8": lambda: run_decode(max(args.steps, 1000), args.seed, "int8"),
              "sweep": lambda: gemm_sweep(args.steps, args.warmup, args.seed,
                                          (args.sweep_m,) if args.sweep_m else (4096, 8192, 16384, 32768, 65536)),
@@ -509,7 +548,7 @@ def main():
         result["config4"] = cfg4(20, 5)
         result["config4_int8"] = cfg4(20, 5, "int8")
         torch.cuda.empty_cache()
-        result["config5"] = run_decode(1000, args.seed)
+        result["config5"] = run_decode(1000, args.seed, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         result["config5_int8"] = run_decode(1000, args.seed, "int8")
         torch.cuda.empty_cache()

@@ -53,6 +53,10 @@ namespace cam {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
+#ifndef CAM_GMM_NT_MAXBM
+#define CAM_GMM_NT_MAXBM 32  // tile heights up to this stream their weights nontemporally
+#endif
+
 constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
 constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
@@ -164,6 +168,11 @@ __device__ __forceinline__ void bar()
 __device__ __forceinline__ void dma16(const void *g, void *lds)
 {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+// the same with the nontemporal cache policy: a stream read once (decode weights) is not kept in L2
+__device__ __forceinline__ void dma16_nt(const void *g, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 2);
 }
 __device__ __forceinline__ void dma4(const void *g, void *lds)
 {
@@ -312,7 +321,12 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
             dma16(p.A + c.ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
         } else if (q < A_LOADS + B_LOADS) {
             const int i = q - A_LOADS;
-            dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
+            // decode tiles: the weights are a stream read once, fetched nontemporally (measured on the
+            // config-5 decode step: 244 vs 274 us)
+            if constexpr (BM <= CAM_GMM_NT_MAXBM)
+                dma16_nt(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
+            else
+                dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
         } else {
             const int d = q - A_LOADS - B_LOADS;
             dma4(p.As + c.gs[d] + (size_t)kc * p.M, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
