@@ -3,7 +3,9 @@
 Default workload (benchmark config 2, "dispatch/combine at the DeepSeek-V3
 one-rank shape"): T=4096 tokens, H=7168, E=256 experts, top-8, router logits
 ~N(0,1) plus a per-expert bias ~N(0,0.5); one step = route -> layout -> count
-exchange -> fp8 1x128 dispatch -> combine of identity-expert bf16 rows.
+exchange -> fp8 1x128 dispatch -> combine of identity-expert bf16 rows, run as
+the plan runs it (camhipMoePrefillDispatch + camhipMoePrefillCombine, four
+launches); the reference-shaped eight-launch chain is timed beside it.
 Inputs are synthetic, seeded, resident in HBM before the timed region.
 
 Prints ONE JSON line (rank 0).  `value` is tokens/s of the whole step;
@@ -174,6 +176,38 @@ FP8_PEAK_TFLOPS = 5000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, POP/s
 
 
+def graph_time(fn, n, warmup, stream):
+    """ms per call of fn (a sequence of launches, no host synchronisation), over exactly n timed calls: fn is
+    captured `reps` times back to back in one HIP graph (reps = the largest of 10, 5, 2, 1 that divides n; a
+    model's forward pass would hold the layer in a larger graph, not replay one graph per layer), after two eager
+    runs on a side stream; the graph is replayed for the warmup, then n / reps times between two HIP events on
+    `stream`."""
+    reps = next(r for r in (10, 5, 2, 1) if n % r == 0)
+    side = torch.cuda.Stream(device=stream.device)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        fn()
+        fn()
+    stream.wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(reps):
+            fn()
+    stream.wait_stream(side)
+    with torch.cuda.stream(stream):
+        for _ in range(max(3, warmup // reps)):
+            graph.replay()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n // reps):
+            graph.replay()
+        b.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return a.elapsed_time(b) / n
+
+
 def zipf_bias(E, s, seed):
     """log-popularity bias: expert popularity ~ 1/rank^s over a seeded permutation of the ids"""
     g = torch.Generator().manual_seed(seed + 17)
@@ -220,37 +254,17 @@ def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
     w1, s1, w2, s2 = make_weights(L, H, I, dtype, dev, seed)
     plan = MoeLayerPlan(T, H, E, K, L, I, dtype=dtype, device=dev)
     stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
 
-    def step(i=None):
-        plan.route(logits, bias)
-        plan.layout()
-        plan.dispatch(x)
-        if i is not None:
-            ev[i][0].record(stream)
+    def step():
+        plan.dispatch_step(logits, x, bias)
         plan.gmm1(w1, s1)
-        if i is not None:
-            ev[i][1].record(stream)
         plan.gmm2(w2, s2)
-        if i is not None:
-            ev[i][2].record(stream)
-        plan.combine(plan.y)
-        if i is not None:
-            ev[i][3].record(stream)
+        plan.combine_step(plan.y)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for i in range(steps):
-        step(i)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
-    g1 = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    g2 = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    # HIP-graph replays (see graph_time): the whole layer, then each GEMM launch alone on the layer's data
+    ms = graph_time(step, steps, warmup, stream)
+    g1 = graph_time(lambda: plan.gmm1(w1, s1), steps, warmup, stream)
+    g2 = graph_time(lambda: plan.gmm2(w2, s2), steps, warmup, stream)
     counts = plan.recv_tokens_per_expert[:L].cpu()
     M = int(counts.sum())
     touched = int((counts > 0).sum())
@@ -478,40 +492,34 @@ def main():
     plan = MoePrefillPlan(T, H, E, K, quant_mode=3, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    n = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    # Every timing below replays a HIP graph of the work: eager launches through the Python binding cost more
+    # host time per step than the GPU needs, which would leave the GPU idle between launches.
+    def step():
+        # the step as the plan runs it: route + layout + count exchange + dispatch in three launches
+        # (camhipMoePrefillDispatch), then the combine gather on the dispatch's row map
+        plan.dispatch_step(logits, x, bias)
+        plan.combine_step(y)
 
-    def step(i=None):
+    def step_ops():
+        # the same step through the reference-shaped calls (eight launches)
         plan.route(logits, bias)
         plan.layout()
-        if i is not None:
-            ev[i][0].record(stream)
         plan.dispatch(x)
-        if i is not None:
-            ev[i][1].record(stream)
         plan.combine(y)
-        if i is not None:
-            ev[i][2].record(stream)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    t_start.record(stream)
-    for i in range(n):
-        step(i)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    ms = t_start.elapsed_time(t_end) / n
-    d_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / n
-    c_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / n
+    n = args.steps
+    ms = graph_time(step, n, args.warmup, stream)
+    rows = int(plan.recv_count[-1].item())
+    assert rows == T * K
+    ds_ms = graph_time(lambda: plan.dispatch_step(logits, x, bias), n, args.warmup, stream)
+    c_ms = graph_time(lambda: plan.combine_step(y), n, args.warmup, stream)
+    ms_ops = graph_time(step_ops, n, args.warmup, stream)
+    d_ms = graph_time(lambda: plan.dispatch(x), n, args.warmup, stream)      # the dispatch launch alone
+    c_ops_ms = graph_time(lambda: plan.combine(y), n, args.warmup, stream)   # scatter + gather
     db, cb = dispatch_bytes(T, H, K), combine_bytes(T, H, K)
     comb_gbps = cb / (c_ms * 1e-3) / 1e9
     disp_gbps = db / (d_ms * 1e-3) / 1e9
     dc_gbps = (db + cb) / ((d_ms + c_ms) * 1e-3) / 1e9
-    rows = int(plan.total_recv.item())
-    assert rows == T * K
 
     result = {
         "metric": METRIC,
@@ -531,14 +539,22 @@ def main():
                    "topk": K, "parallelism": "ep1 (one GPU, no collectives)"},
         "roofline": {"bound": "hbm", "achieved": comb_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": comb_gbps / HBM_PEAK_GBPS,
-                     "traffic": measured_traffic(["combine_scatter_kernel", "combine_gather_kernel"]),
+                     "traffic": measured_traffic(["combine_gather_kernel"]),
                      "traffic_source": "profiles/dispatch_combine_cfg2_hbm_counters.md (rocprofv3 FETCH_SIZE x2.0 + "
                                        "WRITE_SIZE x1.0, same workload)",
-                     "kernel": "combine (scatter+gather)", "algorithmic_bytes": cb},
-        "dispatch": {"ms": d_ms, "GBps": disp_gbps, "frac": disp_gbps / HBM_PEAK_GBPS, "algorithmic_bytes": db},
+                     "kernel": "combine gather (the step's combine launch)", "algorithmic_bytes": cb},
+        "step_launches": "camhipMoePrefillDispatch (route+histogram, scan+count exchange, dispatch) + "
+                         "camhipMoePrefillCombine (gather)",
+        "dispatch_step_ms": ds_ms,
+        "dispatch": {"ms": d_ms, "GBps": disp_gbps, "frac": disp_gbps / HBM_PEAK_GBPS, "algorithmic_bytes": db,
+                     "timed_in": "the reference-op chain (the dispatch launch alone)"},
         "combine": {"ms": c_ms, "GBps": comb_gbps, "frac": comb_gbps / HBM_PEAK_GBPS},
         "dispatch_combine_GBps": dc_gbps,
         "dispatch_combine_frac": dc_gbps / HBM_PEAK_GBPS,
+        "reference_op_chain": {"ms_per_step": ms_ops, "tokens_per_s": T / (ms_ops * 1e-3), "dispatch_ms": d_ms,
+                               "combine_ms": c_ops_ms,
+                               "calls": "camhipMoeRoute, camhipDispatchLayout, camhipNotifyDispatch, "
+                                        "camhipMoeDispatchNormal, camhipMoeCombineNormal (8 launches)"},
     }
     del plan, x, y
     torch.cuda.empty_cache()

@@ -161,6 +161,36 @@ CAMHIP_API camhipStatus camhipMoeCombineNormalGetWorkspaceSize(
 CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                                void *stream);
 
+/* ------------------------------------------------------------------ prefill step (extension)
+ * No reference counterpart: the route -> layout -> count exchange -> dispatch -> combine chain of one EP rank
+ * in four launches instead of eight, for runners that own the whole step (umdk_amd.plan).  The results are
+ * those of the reference-shaped calls above, bit for bit:
+ *   camhipMoePrefillDispatch: camhipMoeRoute over numExperts experts, then, over the localExperts experts
+ *   0..localExperts-1 (other ids are not routed on this rank), the layout, count exchange and
+ *   camhipMoeDispatchNormal.  The per-expert rank of each (t,k) is not materialised (send_token_idx): the
+ *   routing launch writes per-chunk expert histograms, one launch scans them and runs the count exchange,
+ *   and the dispatch ranks each entry inside its chunk.  Outputs: topkIdx/topkWeights [numTokens, topK],
+ *   recvX and recvXScales as the dispatch call's quantMode (0, 2, 3, 5), expandIdx [rows, 3], recvCount
+ *   [localExperts] (inclusive prefix), recvTokensPerExpert [localExperts] int64, and combineRowMap
+ *   [numTokens, topK] = the row of (t,k), or -1, which replaces the combine's own scatter pass.
+ *   camhipMoePrefillCombine: camhipMoeCombineNormal on those outputs (y [rows, hidden] bf16 expert outputs in
+ *   dispatch order), reading combineRowMap instead of building it.
+ * Limits: numTokens in [1,65536], topK <= 16, localExperts <= numExperts <= 512, recvRowsCapacity in
+ * [1, numTokens * topK]. */
+CAMHIP_API camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(
+    const float *logits, const float *bias, const uint16_t *x, int64_t numTokens, int64_t hidden, int64_t numExperts,
+    int64_t localExperts, int64_t topK, int64_t quantMode, int64_t recvRowsCapacity, int32_t *topkIdx,
+    float *topkWeights, void *recvX, float *recvXScales, int32_t *expandIdx, int32_t *recvCount,
+    int64_t *recvTokensPerExpert, int32_t *combineRowMap, uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoePrefillDispatch(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                                 void *stream);
+CAMHIP_API camhipStatus camhipMoePrefillCombineGetWorkspaceSize(
+    const uint16_t *y, const int32_t *expandIdx, const int32_t *combineRowMap, const int32_t *recvCount,
+    const float *topkWeights, int64_t numTokens, int64_t topK, int64_t hidden, int64_t localExperts,
+    int64_t recvRowsCapacity, uint16_t *out, uint64_t *workspaceSize, camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoePrefillCombine(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                                void *stream);
+
 /* Allocation-free combine.  No reference counterpart: for callers that cannot allocate or pass a
  * workspace (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * The same arguments and results as camhipMoeCombineNormalGetWorkspaceSize + camhipMoeCombineNormal in

@@ -27,6 +27,8 @@ SIGNATURES = {
     "camhipGroupedMatmulSwiglu": "ppp iiii pp iii pp",
     "camhipGroupedMatmul": "ppp iiii pp ii p",
     "camhipFusedDeepMoe": "pppppp p pppp ppp iiiiii iiiii ppp",
+    "camhipMoePrefillDispatch": "ppp iiiiiii pppppppp",
+    "camhipMoePrefillCombine": "ppppp iiiii p",
 }
 
 _lib = None

@@ -368,6 +368,121 @@ camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspaceSize, cam
     return run_executor("moe_combine", workspace, workspaceSize, executor, stream);
 }
 
+// ---------------------------------------------------------------- prefill step (extension)
+camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(const float *logits, const float *bias, const uint16_t *x,
+                                                      int64_t numTokens, int64_t hidden, int64_t numExperts,
+                                                      int64_t localExperts, int64_t topK, int64_t quantMode,
+                                                      int64_t recvRowsCapacity, int32_t *topkIdx, float *topkWeights,
+                                                      void *recvX, float *recvXScales, int32_t *expandIdx,
+                                                      int32_t *recvCount, int64_t *recvTokensPerExpert,
+                                                      int32_t *combineRowMap, uint64_t *workspaceSize,
+                                                      camhipExecutor **executor)
+{
+    CHECK_PARAM(numTokens >= 1 && numTokens <= kMaxTokens, "moe_prefill_dispatch: numTokens %lld out of [1,%lld]",
+                (long long)numTokens, (long long)kMaxTokens);
+    CHECK_PARAM(numExperts >= 1 && numExperts <= kMaxExperts, "moe_prefill_dispatch: numExperts %lld out of range",
+                (long long)numExperts);
+    CHECK_PARAM(localExperts >= 1 && localExperts <= numExperts,
+                "moe_prefill_dispatch: localExperts %lld out of [1, numExperts]", (long long)localExperts);
+    CHECK_PARAM(topK >= 1 && topK <= kMaxTopk && topK <= numExperts, "moe_prefill_dispatch: topK %lld out of range",
+                (long long)topK);
+    CHECK_PARAM(hidden >= kMinHidden && hidden <= kMaxHidden && hidden % 16 == 0,
+                "moe_prefill_dispatch: hidden %lld must be in [%lld,%lld] and a multiple of 16", (long long)hidden,
+                (long long)kMinHidden, (long long)kMaxHidden);
+    CHECK_PARAM(quantMode == CAMHIP_QUANT_NONE || quantMode == CAMHIP_QUANT_INT8_TOKEN ||
+                    quantMode == CAMHIP_QUANT_FP8_BLOCK || quantMode == CAMHIP_QUANT_FP8_BLOCK_KMAJOR,
+                "moe_prefill_dispatch: quantMode %lld not supported (0, 2, 3 or 5)", (long long)quantMode);
+    const bool kmajor = quantMode == CAMHIP_QUANT_FP8_BLOCK_KMAJOR;
+    const int q = kmajor ? CAMHIP_QUANT_FP8_BLOCK : (int)quantMode;
+    CHECK_PARAM(q != CAMHIP_QUANT_FP8_BLOCK || hidden % 128 == 0,
+                "moe_prefill_dispatch: fp8 1x128 quantisation needs hidden %% 128 == 0 (hidden %lld)",
+                (long long)hidden);
+    CHECK_PARAM(recvRowsCapacity >= 1 && recvRowsCapacity <= numTokens * topK,
+                "moe_prefill_dispatch: recvRowsCapacity %lld out of [1, numTokens * topK]",
+                (long long)recvRowsCapacity);
+    CHECK_PTR(logits);
+    CHECK_PTR(x);
+    CHECK_PTR(topkIdx);
+    CHECK_PTR(topkWeights);
+    CHECK_PTR(recvX);
+    CHECK_PTR(expandIdx);
+    CHECK_PTR(recvCount);
+    CHECK_PTR(recvTokensPerExpert);
+    CHECK_PTR(combineRowMap);
+    if (q != CAMHIP_QUANT_NONE)
+        CHECK_PTR(recvXScales);
+    const int T = (int)numTokens, H = (int)hidden, E = (int)numExperts, L = (int)localExperts, K = (int)topK;
+    const int cap = (int)recvRowsCapacity;
+    const int tpc = cam::route_tokens_per_block();
+    const int nc = (T + tpc - 1) / tpc;
+    // workspace: chunk counts -> chunk bases [L][nc], send offsets [L], expert totals [L], the arrival count
+    const uint64_t counts_bytes = ((uint64_t)L * nc * sizeof(int32_t) + 255) & ~(uint64_t)255;
+    const uint64_t vec_bytes = ((uint64_t)L * sizeof(int32_t) + 255) & ~(uint64_t)255;
+    const uint64_t ws = counts_bytes + 2 * vec_bytes + sizeof(uint32_t);
+    return make_executor(
+        ws,
+        [=](void *w, hipStream_t s) {
+            int32_t *counts = (int32_t *)w;
+            int32_t *send_off = (int32_t *)((uint8_t *)w + counts_bytes);
+            int32_t *totals = (int32_t *)((uint8_t *)w + counts_bytes + vec_bytes);
+            uint32_t *arrivals = (uint32_t *)((uint8_t *)w + counts_bytes + 2 * vec_bytes);
+            hipError_t e =
+                cam::launch_route_hist(logits, bias, T, E, K, L, topkIdx, topkWeights, counts, arrivals, s);
+            if (e != hipSuccess)
+                return e;
+            e = cam::launch_scan_notify(L, nc, counts, totals, arrivals, send_off, recvCount, recvTokensPerExpert,
+                                        s);
+            if (e != hipSuccess)
+                return e;
+            return cam::launch_dispatch(x, topkIdx, send_off, nullptr, T, H, K, L, 0, cap, q, recvX, recvXScales,
+                                        expandIdx, s, combineRowMap, nullptr, kmajor, counts, tpc);
+        },
+        workspaceSize, executor);
+}
+
+camhipStatus camhipMoePrefillDispatch(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return run_executor("moe_prefill_dispatch", workspace, workspaceSize, executor, stream);
+}
+
+camhipStatus camhipMoePrefillCombineGetWorkspaceSize(const uint16_t *y, const int32_t *expandIdx,
+                                                     const int32_t *combineRowMap, const int32_t *recvCount,
+                                                     const float *topkWeights, int64_t numTokens, int64_t topK,
+                                                     int64_t hidden, int64_t localExperts, int64_t recvRowsCapacity,
+                                                     uint16_t *out, uint64_t *workspaceSize,
+                                                     camhipExecutor **executor)
+{
+    CHECK_PARAM(numTokens >= 1 && numTokens <= kMaxTokens, "moe_prefill_combine: numTokens %lld out of [1,%lld]",
+                (long long)numTokens, (long long)kMaxTokens);
+    CHECK_PARAM(topK >= 1 && topK <= kMaxTopk, "moe_prefill_combine: topK %lld out of range", (long long)topK);
+    CHECK_PARAM(hidden >= kMinHidden && hidden <= kMaxHidden && hidden % 16 == 0,
+                "moe_prefill_combine: hidden %lld must be in [%lld,%lld] and a multiple of 16", (long long)hidden,
+                (long long)kMinHidden, (long long)kMaxHidden);
+    CHECK_PARAM(localExperts >= 1 && localExperts <= kMaxExperts, "moe_prefill_combine: localExperts out of range");
+    CHECK_PARAM(recvRowsCapacity >= 1 && recvRowsCapacity <= numTokens * topK,
+                "moe_prefill_combine: recvRowsCapacity %lld out of [1, numTokens * topK]",
+                (long long)recvRowsCapacity);
+    CHECK_PTR(y);
+    CHECK_PTR(expandIdx);
+    CHECK_PTR(combineRowMap);
+    CHECK_PTR(recvCount);
+    CHECK_PTR(topkWeights);
+    CHECK_PTR(out);
+    const int T = (int)numTokens, K = (int)topK, H = (int)hidden, N = (int)recvRowsCapacity;
+    const int32_t *last = recvCount + (localExperts - 1);
+    return make_executor(
+        0,
+        [=](void *, hipStream_t s) {
+            return cam::launch_combine_gather(y, expandIdx, N, last, topkWeights, T, K, H, out, combineRowMap, s);
+        },
+        workspaceSize, executor);
+}
+
+camhipStatus camhipMoePrefillCombine(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return run_executor("moe_prefill_combine", workspace, workspaceSize, executor, stream);
+}
+
 camhipStatus camhipMoeCombineNormalNoAlloc(const uint16_t *recvX, const int32_t *tokenSrcInfo, int64_t numRecvRows,
                                            const int32_t *epRecvCounts, const float *recvTopkWeights, int64_t numTokens,
                                            int64_t numTopk, int64_t hidden, int64_t epWorldSize, int64_t epRankId,

@@ -22,7 +22,16 @@
 
 namespace cam {
 
-constexpr int COMB_WAVES = 4;
+#ifndef CAM_COMB_WAVES
+#define CAM_COMB_WAVES 4
+#endif
+#ifndef CAM_COMB_NTLD
+#define CAM_COMB_NTLD 1
+#endif
+#ifndef CAM_COMB_NTST
+#define CAM_COMB_NTST 1
+#endif
+constexpr int COMB_WAVES = CAM_COMB_WAVES;
 constexpr int COMB_NIT = 7;   // H <= 7168
 constexpr int COMB_KB = 8;    // rows in flight per batch
 
@@ -80,9 +89,14 @@ __global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
             wk[b] = __shfl(w, k < K ? k : 0, 64);
             if (rk[b] >= 0 && act) {
                 const uint16_t *src = y + (size_t)rk[b] * H + col;
+#if CAM_COMB_NTLD
                 v[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src));
                 v[b][1] = act1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + 512))
                                : u32x4{0, 0, 0, 0};
+#else
+                v[b][0] = *reinterpret_cast<const u32x4 *>(src);
+                v[b][1] = act1 ? *reinterpret_cast<const u32x4 *>(src + 512) : u32x4{0, 0, 0, 0};
+#endif
             }
         }
 #pragma unroll
@@ -101,9 +115,15 @@ __global__ __launch_bounds__(COMB_WAVES * 64) void combine_gather_kernel(
     }
     if (act) {
         uint16_t *orow = out + (size_t)t * H + col;
+#if CAM_COMB_NTST
         __builtin_nontemporal_store(pack_bf16x8(acc), reinterpret_cast<u32x4 *>(orow));
         if (act1)
             __builtin_nontemporal_store(pack_bf16x8(acc + 8), reinterpret_cast<u32x4 *>(orow + 512));
+#else
+        *reinterpret_cast<u32x4 *>(orow) = pack_bf16x8(acc);
+        if (act1)
+            *reinterpret_cast<u32x4 *>(orow + 512) = pack_bf16x8(acc + 8);
+#endif
     }
 }
 

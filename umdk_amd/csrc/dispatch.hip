@@ -26,31 +26,68 @@ constexpr int DISP_WAVES = 4;
 constexpr int DISP_NIT = 7;  // H <= 7168 = 7 * 1024
 constexpr int DISP_MAX_K = 16;
 
+// Where the rank of (t,k) within its expert comes from: send_token_idx[t,k] (the layout op's output), or,
+// with send_token_idx == nullptr, chunk_base (the prefill step: chunks of `tpc` tokens, chunk_base[e * nc + c]
+// = entries of expert e in chunks before c) plus the rank inside the chunk, counted here.
+struct RankSrc {
+    const int32_t *send_token_idx;
+    const int32_t *chunk_base;
+    int tpc;
+};
+
 // Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
 __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
-                                             const int32_t *__restrict__ send_offset,
-                                             const int32_t *__restrict__ send_token_idx, int t, int K, int E,
-                                             int cap, int lane)
+                                             const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
+                                             int T, int K, int E, int cap, int lane)
 {
     int dst = -1;
     if (topk_idx == nullptr)  // identity mode (K = 1): row t of x quantised into row t
         return lane == 0 ? t : -1;
-    if (lane < K) {
-        const int e = topk_idx[(size_t)t * K + lane];
-        if (e >= 0 && e < E) {
-            dst = send_offset[e] + send_token_idx[(size_t)t * K + lane];
-            if (dst < 0 || dst >= cap)  // inconsistent counts: never write outside the output
-                dst = -1;
+    if (rs.send_token_idx) {
+        if (lane < K) {
+            const int e = topk_idx[(size_t)t * K + lane];
+            if (e >= 0 && e < E)
+                dst = send_offset[e] + rs.send_token_idx[(size_t)t * K + lane];
+        }
+    } else {
+        // rank inside the chunk (at most 256 entries, row-major (t,k) order): per k, one ballot per 64-entry
+        // window of the chunk's ids marks the entries of the same expert, and those before (t,k) are counted
+        const int c = t / rs.tpc, t0 = c * rs.tpc, nc = (T + rs.tpc - 1) / rs.tpc;
+        const int p0 = t0 * K, pn = min(T, t0 + rs.tpc) * K - p0;
+        int ids[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = u * 64 + lane;
+            const int v = i < pn ? topk_idx[p0 + i] : -1;
+            ids[u] = (v >= 0 && v < E) ? v : -1;
+        }
+        for (int k = 0; k < K; ++k) {
+            const int e = __builtin_amdgcn_readfirstlane(topk_idx[(size_t)t * K + k]);
+            if (e < 0 || e >= E)
+                continue;
+            const int q = (t - t0) * K + k;  // this entry's position in the chunk
+            int cnt = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint64_t m = __ballot(ids[u] == e);
+                const int n = q - u * 64;
+                const uint64_t before = n >= 64 ? ~0ull : n <= 0 ? 0ull : ((1ull << n) - 1);
+                cnt += __popcll(m & before);
+            }
+            if (lane == k)
+                dst = send_offset[e] + rs.chunk_base[(size_t)e * nc + c] + cnt;
         }
     }
-    return dst;
+    if (dst >= cap)  // inconsistent counts: never write outside the output
+        dst = -1;
+    return dst < 0 ? -1 : dst;
 }
 
 // bf16 copy and fp8 1x128 quantisation: one wave per (token, 1024-column chunk).
 template <int MODE>
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
-    const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap, int nchunk,
+    RankSrc rs, int T, int H, int K, int E, int rank, int cap, int nchunk,
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
     int32_t *__restrict__ inv_out, int kmajor)
 {
@@ -60,9 +97,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     if (item >= (long)T * nchunk)
         return;
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
-    const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
-    if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
-        inv_out[(size_t)t * K + lane] = dst;
+    // the slice of x is requested first, so its loads are in flight while the destination rows resolve
     if constexpr (MODE == QUANT_NONE) {
         // lane l copies columns [1024 j + 8 l, +8) and [1024 j + 512 + 8 l, +8): each 16-byte
         // store instruction of the wave writes one contiguous kilobyte
@@ -74,6 +109,9 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
             if (act1)
                 raw1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col + 512));
         }
+        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+        if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
+            inv_out[(size_t)t * K + lane] = dst;
         for (int k = 0; k < K; ++k) {
             const int row = __shfl(dst, k, 64);
             if (row < 0)
@@ -102,6 +140,9 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
             raw0 = src[0];
             raw1 = src[1];
         }
+        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+        if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
+            inv_out[(size_t)t * K + lane] = dst;
         float f[16];
         unpack_bf16x8(raw0, f);
         unpack_bf16x8(raw1, f + 8);
@@ -146,7 +187,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
 template <bool FUSED>
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
-    const int32_t *__restrict__ send_token_idx, int T, int H, int K, int E, int rank, int cap,
+    RankSrc rs, int T, int H, int K, int E, int rank, int cap,
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
     int32_t *__restrict__ inv_out, const float *__restrict__ smooth)
 {
@@ -155,7 +196,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const int t = blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
     if (t >= T)
         return;
-    const int dst = dispatch_dest(topk_idx, send_offset, send_token_idx, t, K, E, cap, lane);
+    const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
     if (inv_out && lane < K)
         inv_out[(size_t)t * K + lane] = dst;
     const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)t * H);
@@ -255,8 +296,11 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out,
-                           const float *smooth, bool kmajor_scales)
+                           const float *smooth, bool kmajor_scales, const int32_t *chunk_base, int tpc)
 {
+    if (topk_idx && !send_token_idx && (!chunk_base || tpc < 1 || tpc * K > 256))
+        return hipErrorInvalidValue;
+    const RankSrc rs{send_token_idx, chunk_base, tpc};
     if (T == 0)
         return hipSuccess;
     if (H > DISP_NIT * 1024 || K > DISP_MAX_K || (H & 15))
@@ -268,23 +312,23 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
     switch (quant_mode) {
     case QUANT_NONE:
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_NONE>, grid_chunk, block, 0, s, x, topk_idx, send_offset,
-                           send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out, 0);
+                           rs, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out, 0);
         break;
     case QUANT_INT8_TOKEN:
         hipLaunchKernelGGL(dispatch_int8_kernel<false>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
-                           topk_idx, send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx,
+                           topk_idx, send_offset, rs, T, H, K, E, rank, cap, ex, scales, expand_idx,
                            inv_out, nullptr);
         break;
     case QUANT_INT8_FUSED:
         hipLaunchKernelGGL(dispatch_int8_kernel<true>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
-                           topk_idx, send_offset, send_token_idx, T, H, K, E, rank, cap, ex, scales, expand_idx,
+                           topk_idx, send_offset, rs, T, H, K, E, rank, cap, ex, scales, expand_idx,
                            inv_out, smooth);
         break;
     case QUANT_FP8_BLOCK:
         if (H & 127)
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_FP8_BLOCK>, grid_chunk, block, 0, s, x, topk_idx,
-                           send_offset, send_token_idx, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out,
+                           send_offset, rs, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out,
                            kmajor_scales ? 1 : 0);
         break;
     default:

@@ -14,6 +14,13 @@ enum QuantMode { QUANT_NONE = 0, QUANT_INT8_TOKEN = 2, QUANT_FP8_BLOCK = 3, QUAN
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
                         float *topk_w, hipStream_t s, int64_t *topk_idx64 = nullptr);
 
+// routing that also writes per-chunk histograms of the ids below Ec: chunks of route_tokens_per_block() tokens,
+// chunk_counts[e * nc + c] (the prefill step)
+int route_tokens_per_block();
+// (*arrivals is cleared for the launch_scan_notify that follows)
+hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
+                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, hipStream_t s);
+
 // ---- dispatch layout (layout.hip)
 struct LayoutPlan {
     int tokens_per_chunk;
@@ -24,6 +31,10 @@ size_t layout_workspace_bytes(int T, int K, int E, int R);
 hipError_t launch_layout(const int64_t *topk_idx, int T, int K, int E, int R, int32_t *ntok_per_rank,
                          int32_t *ntok_per_expert, int32_t *is_token_in_rank, int32_t *send_token_idx,
                          void *ws, hipStream_t s);
+// the prefill step: chunk counts [E][nc] -> exclusive chunk bases in place, row totals [E], then the one-rank
+// count exchange (run by the last block to arrive; *arrivals must be 0 at launch)
+hipError_t launch_scan_notify(int E, int nc, int32_t *counts, int32_t *totals, uint32_t *arrivals,
+                              int32_t *send_offset, int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s);
 // int32 topk ids, used by the fused path
 hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
                              int32_t *send_token_idx, void *ws, hipStream_t s);
@@ -45,7 +56,10 @@ hipError_t launch_notify(const int32_t *counts, int E, int T, int32_t *send_offs
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
-                           int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false);
+                           int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false,
+                           const int32_t *chunk_base = nullptr, int tpc = 0);
+// (send_token_idx == nullptr: the rank within the expert is chunk_base[e * nc + t / tpc] plus the rank inside the
+// token's chunk of tpc tokens, counted in the kernel; tpc * K <= 256)
 // (fp8: kmajor_scales writes the block scales as [H/128, cap], the layout the grouped GEMMs read)
 // combine without the scatter launch, for callers whose dispatch already wrote inv
 hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,

@@ -46,12 +46,16 @@ __device__ __forceinline__ uint32_t order_key(float s)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-template <int PER>
+// HIST: the block's 16 tokens are one layout chunk; it also writes the chunk's histogram of the picked
+// ids below Ec (the local experts), chunk_counts[e * gridDim.x + blockIdx.x] for every e < Ec
+template <int PER, bool HIST = false>
 __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int T, int E,
                                                                  int K, int32_t *__restrict__ topk_idx,
                                                                  float *__restrict__ topk_w,
-                                                                 int64_t *__restrict__ topk_idx64)
+                                                                 int64_t *__restrict__ topk_idx64,
+                                                                 int Ec = 0, int32_t *__restrict__ chunk_counts = nullptr,
+                                                                 uint32_t *__restrict__ arrivals = nullptr)
 {
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
@@ -123,6 +127,19 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
         if (topk_idx64)
             topk_idx64[(size_t)t * K + l16] = my_idx;
     }
+    if constexpr (HIST) {
+        if (blockIdx.x == 0 && threadIdx.x == 0)
+            *arrivals = 0u;  // the arrival count of the scan launch that follows on the stream
+        __shared__ int32_t hist[ROUTE_MAX_PER_LANE * 16];
+        for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
+            hist[e] = 0;
+        __syncthreads();
+        if (l16 < K && live && my_idx < Ec)
+            atomicAdd(&hist[my_idx], 1);  // counts only: the order of the adds does not matter
+        __syncthreads();
+        for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
+            chunk_counts[(size_t)e * gridDim.x + blockIdx.x] = hist[e];
+    }
 }
 
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
@@ -148,6 +165,37 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
         hipLaunchKernelGGL(route_kernel<16>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
     else
         hipLaunchKernelGGL(route_kernel<32>, g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, topk_idx64);
+    return hipGetLastError();
+}
+
+int route_tokens_per_block() { return ROUTE_WAVES * 4; }
+
+hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
+                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, hipStream_t s)
+{
+    if (T == 0)
+        return hipSuccess;
+    if (E > 16 * ROUTE_MAX_PER_LANE || K > 16 || Ec > E || Ec < 1)
+        return hipErrorInvalidValue;
+    const int grid = (T + ROUTE_WAVES * 4 - 1) / (ROUTE_WAVES * 4);
+    const dim3 g(grid), b(ROUTE_WAVES * 64);
+    const int per = (E + 15) >> 4;
+#define ROUTE_HIST_CASE(P)                                                                                          \
+    hipLaunchKernelGGL((route_kernel<P, true>), g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, nullptr, Ec,   \
+                       chunk_counts, arrivals)
+    if (per <= 1)
+        ROUTE_HIST_CASE(1);
+    else if (per <= 2)
+        ROUTE_HIST_CASE(2);
+    else if (per <= 4)
+        ROUTE_HIST_CASE(4);
+    else if (per <= 8)
+        ROUTE_HIST_CASE(8);
+    else if (per <= 16)
+        ROUTE_HIST_CASE(16);
+    else
+        ROUTE_HIST_CASE(32);
+#undef ROUTE_HIST_CASE
     return hipGetLastError();
 }
 

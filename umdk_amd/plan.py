@@ -44,6 +44,13 @@ class MoePrefillPlan:
         ws_dispatch = _lib.workspace_size("camhipMoeDispatchNormal", 1, 1, 1, 1, None, None, T, H, K, 1, 0, E,
                                           quant_mode, N, 1, 1, 1, 1)
         self.ws_layout = torch.empty(max(ws_layout, 1), dtype=torch.uint8, device=dev)
+        # the four-launch step (camhipMoePrefillDispatch / camhipMoePrefillCombine): the combine's row map
+        # comes from the dispatch
+        self.combine_row_map = torch.empty((T, K), **i32)
+        self.E_route = E
+        ws_step = _lib.workspace_size("camhipMoePrefillDispatch", 1, None, 1, T, H, E, E, K, quant_mode, N,
+                                      1, 1, 1, 1, 1, 1, 1, 1)
+        self.ws_step = torch.empty(max(ws_step, 1), dtype=torch.uint8, device=dev)
         self.ws_combine = torch.empty(max(ws_combine, 1), dtype=torch.uint8, device=dev)
         self.ws_dispatch = torch.empty(max(ws_dispatch, 1), dtype=torch.uint8, device=dev)
 
@@ -82,6 +89,26 @@ class MoePrefillPlan:
         return self.out
 
 
+    # -- the step in four launches ------------------------------------------------
+    def dispatch_step(self, logits, x, bias=None, stream=None):
+        """route (over E_route experts) + layout + count exchange + dispatch (over the local experts) in three
+        launches; the same results as route(), layout() and dispatch() (send_token_idx and num_tokens_per_expert
+        are not produced), plus the combine's row map."""
+        _lib.launch("camhipMoePrefillDispatch", logits.data_ptr(), None if bias is None else bias.data_ptr(),
+                    x.data_ptr(), self.T, self.H, self.E_route, self.E, self.K, self.q, self.N,
+                    self.topk_idx.data_ptr(), self.topk_w.data_ptr(), self.expand_x.data_ptr(),
+                    None if self.q == QUANT_NONE else self.scales.data_ptr(), self.expand_idx.data_ptr(),
+                    self.recv_count.data_ptr(), self.recv_tokens_per_expert.data_ptr(),
+                    self.combine_row_map.data_ptr(), workspace=self.ws_step, stream=stream, device=self.device)
+
+    def combine_step(self, y, stream=None):
+        """combine() after dispatch_step(): one gather launch on the dispatch's row map."""
+        _lib.launch("camhipMoePrefillCombine", y.data_ptr(), self.expand_idx.data_ptr(),
+                    self.combine_row_map.data_ptr(), self.recv_count.data_ptr(), self.topk_w.data_ptr(), self.T,
+                    self.K, self.H, self.E, self.N, self.out.data_ptr(), stream=stream, device=self.device)
+        return self.out
+
+
 class MoeLayerPlan(MoePrefillPlan):
     """Full expert layer on one EP rank: route over `E` experts, keep the
     (t,k) pairs whose expert is one of this rank's `L` local experts (ids
@@ -102,8 +129,8 @@ class MoeLayerPlan(MoePrefillPlan):
         if dtype not in _check:
             raise ValueError(f"MoeLayerPlan: dtype must be bf16, fp8 or int8 (got {dtype})")
         q = _check[dtype]
-        self.E_route = E
         super().__init__(T, H, L, K, quant_mode=q, device=device)
+        self.E_route = E
         self.L, self.I, self.dtype = L, I, dtype
         dev = self.device
         N = self.N
@@ -162,6 +189,13 @@ class MoeLayerPlan(MoePrefillPlan):
         return self.y
 
     def forward(self, x, logits, bias, w1, w1_scale, w2, w2_scale, stream=None):
+        """The whole layer: dispatch_step, GMM1 + SwiGLU, GMM2, combine_step (six launches for fp8/bf16)."""
+        self.dispatch_step(logits, x, bias, stream)
+        self.experts(w1, w1_scale, w2, w2_scale, stream)
+        return self.combine_step(self.y, stream)
+
+    def forward_op_chain(self, x, logits, bias, w1, w1_scale, w2, w2_scale, stream=None):
+        """The same layer through the reference-shaped calls (route, layout, count exchange, dispatch, ..., combine)."""
         self.route(logits, bias, stream)
         self.layout(stream)
         self.dispatch(x, stream)
