@@ -559,14 +559,16 @@ def main():
     del plan, x, y
     torch.cuda.empty_cache()
     if args.config in ("default", "all"):
+        # the decode step first: its weight stream is measured on weights allocated before the larger
+        # configurations have cycled memory through the caching allocator, as a server allocates them at start-up
+        result["config5"] = run_decode(1000, args.seed, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        result["config5_int8"] = run_decode(1000, args.seed, "int8")
+        torch.cuda.empty_cache()
         result["config3"] = cfg3(10, 3)
         torch.cuda.empty_cache()
         result["config4"] = cfg4(20, 5)
         result["config4_int8"] = cfg4(20, 5, "int8")
-        torch.cuda.empty_cache()
-        result["config5"] = run_decode(1000, args.seed, cpu=not args.no_cpu)
-        torch.cuda.empty_cache()
-        result["config5_int8"] = run_decode(1000, args.seed, "int8")
         torch.cuda.empty_cache()
     if args.config in ("default", "all"):
         result["measured_peaks"] = measured_peaks()
