@@ -195,8 +195,11 @@ __device__ __forceinline__ void lds_sync()
 }
 
 // Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
-// (first < 0: balanced placement, see below)
-template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first)
+// (first < 0: balanced placement, see below), preceded by a run of rn tiles rs, rs + rstride, ... (an
+// increasing sequence: the first index past the class's tiles ends it).
+template <int DT, int EPI, int BM>
+__device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first, int rs = 0, int rn = 0,
+                                         int rstride = 1)
 {
     using TC = Tile<BM>;
     constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
@@ -237,6 +240,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         G = g_eff;
         logical = (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
     }
+    // the block's k-th tile: the run, then the strided sequence
+    auto seq = [&](int k) { return k < rn ? rs + k * rstride : logical + (k - rn) * G; };
 
     // DMA slot of this lane inside a 1 KiB band (8 rows x 128 B): row l/8, physical chunk l%8,
     // which holds logical chunk (l%8) ^ ((row >> 1) & 7) -- see swz()
@@ -468,7 +473,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         // drains at its end.
         static_assert(GSTAGES == 2, "two-stage ring");
         constexpr int AHEAD = 2;
-        for (int tile = logical; tile < total; tile += G) {
+        for (int kt = 0, tile = seq(0); tile < total; tile = seq(++kt)) {
             Ctx c;
             setup(tile, c);
             clear_acc();
@@ -587,7 +592,8 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         // with its operands already in flight.  With fewer k-steps than stages, or no next tile, the
         // past-the-end DMAs reload the tile's last k-step (the DMA count per k-step, and so every
         // vmcnt wait, stays uniform) and the ring is drained before the next tile.
-        int tile = logical;
+        int kt = 0;
+        int tile = seq(0);
         if (tile >= total)
             return;
         Ctx cur, nxt;
@@ -595,7 +601,7 @@ template <int DT, int EPI, int BM> __device__ __forceinline__ void gmm_body(cons
         int kb = 0;          // the block's k-steps before the current tile
         bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
         while (true) {
-            const int ntile = tile + G;
+            const int ntile = seq(++kt);
             const bool has_next = ntile < total;
             // (int8: the dequantisation's vector loads would wait for the next tile's DMAs, so no chaining)
             const bool chain = !INT8 && has_next && nk >= GSTAGES;
@@ -884,6 +890,36 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     const int n_heavy = red[0];
     __syncthreads();
     const int G = gridDim.x;
+    // 256-row tiles: heavy M-tiles x N-tiles
+    const int heavy_tiles = n_heavy * (EPI != EPI_PLAIN ? p.N / 2 / 128 : p.N / 256);
+    if (heavy_tiles > 0 && heavy_tiles < G && (G & 7) == 0) {
+        // Fewer heavy tiles than blocks.  They are split evenly over the 8 XCDs (XCD x takes the run
+        // [x hx, (x + 1) hx), consecutive tiles sharing that XCD's L2), so each XCD keeps some blocks free.
+        // The free blocks start on the light tiles at once, `run` in a row each (a 256-row tile costs
+        // about that many weight-streaming 128-row tiles: 2 for 1-byte operands, 1 for bf16); the rest of
+        // the light tiles go round-robin over all blocks in launch order (every XCD in turn), reaching the
+        // heavy blocks as they finish.
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, S = G >> 3;
+        const int hx = (heavy_tiles + 7) / 8;
+        auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
+        const int len = heavy_in(xcd);
+        if (slot < len) {
+            gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, 0x3fffffff, xcd * hx + slot,
+                                   (len - slot + S - 1) / S, S);
+            __syncthreads();  // every wave is done with the first class's ring and table
+        }
+        constexpr int run = DT == DT_BF16 ? 1 : 2;
+        int free_before = 0, free_all = 0;
+        for (int x = 0; x < 8; ++x) {
+            const int fx = max(0, S - heavy_in(x));
+            free_before += x < xcd ? fx : 0;
+            free_all += fx;
+        }
+        const bool is_free = slot >= len;
+        gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
+                               is_free ? (free_before + slot - len) * run : 0, is_free ? run : 0);
+        return;
+    }
     if (n_heavy > 0) {
         gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
         __syncthreads();  // every wave is done with the first class's ring and table
