@@ -247,6 +247,27 @@ def test_diagnose_cost_stats_accumulate(ops):
     torch.cuda.synchronize()
     assert int(ds.item()) >= d1 + 5 and int(cs.item()) >= c1 + 5
 
+    # the value itself: each call adds the phase's microseconds on the stream, so over n calls the counters
+    # track HIP events placed around the same calls (each call truncates to whole microseconds, and the events
+    # also hold the two clock-stamp launches)
+    n = 20
+    ds.zero_()
+    cs.zero_()
+    st = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
+    for e in ev:
+        e[0].record(st)
+        plan.dispatch(x, cost_stats=ds)
+        e[1].record(st)
+        e[2].record(st)
+        plan.combine(y, cost_stats=cs)
+        e[3].record(st)
+    torch.cuda.synchronize()
+    d_ev = sum(e[0].elapsed_time(e[1]) for e in ev) * 1e3
+    c_ev = sum(e[2].elapsed_time(e[3]) for e in ev) * 1e3
+    for got, want in ((int(ds.item()), d_ev), (int(cs.item()), c_ev)):
+        assert 0.75 * want - n <= got <= want + n, (got, want)
+
 
 def test_route_int64_copy_of_ids(ops):
     # the optional int64 output of the route op carries the same ids (the layout op's input type)
