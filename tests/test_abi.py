@@ -189,7 +189,7 @@ def test_converted_weights_cached_per_source():
     assert ops._kmajor(w, 4, 3, "w") is a
     w.add_(1)
     b = ops._kmajor(w, 4, 3, "w")
-    assert b is not a and torch.equal(b, w.t())
+    assert b is a and b.data_ptr() == a.data_ptr() and torch.equal(b, w.t())   # refreshed in place
     v = w.t().contiguous().t()                                  # k-contiguous storage underneath: no copy
     assert ops._kmajor(v, 4, 3, "v").data_ptr() == v.data_ptr()
     n = len(ops._CONVERTED)

@@ -295,9 +295,10 @@ def _converted(src, tag, make):
 
     The result is cached on the source tensor object and its version counter, so a caller that passes
     the same weights on every step (the reference's dynamic-EPLB lists, test_fused_deep_moe.py:256-269)
-    pays the copy once, keeps one stable device address (a captured graph reads it) and re-converts only
-    after the source is modified in place.  The entry is dropped when the source is freed.  A conversion
-    first needed inside graph capture is refused: the copy would land in the graph's private pool."""
+    pays the copy once and keeps one stable device address (a captured graph reads it).  After the source is
+    modified in place, the next eager call refreshes the copy in place (same address, so graphs captured on it
+    replay the new values from then on).  The entry is dropped when the source is freed.  A conversion first
+    needed inside graph capture is refused: the copy would land in the graph's private pool."""
     key = (id(src), tag)
     ent = _CONVERTED.get(key)
     if ent is not None and ent[0]() is src and ent[1] == src._version:
@@ -305,6 +306,12 @@ def _converted(src, tag, make):
     _check(not (src.is_cuda and torch.cuda.is_current_stream_capturing()),
            f"fused_deep_moe: {tag} needs a converted copy (layout or dtype) that cannot be made inside graph "
            "capture; run the call once eagerly before capturing, or pass the kernels' own layout")
+    if ent is not None and ent[0]() is src:
+        # the source changed in place: refresh the copy in place, so graphs captured on it see the new values
+        out = ent[2]
+        out.copy_(make())
+        _CONVERTED[key] = (ent[0], src._version, out)
+        return out
     out = make()
 
     def _drop(_ref, key=key):
