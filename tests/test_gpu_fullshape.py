@@ -4,6 +4,9 @@
   fused_deep_moe -- eagerly and as the route + fused-op HIP graph the benchmark replays.
 * Config 4 (prefill layer): MoeLayerPlan fp8 at T=4096, H=7168, 32 of 256 experts, I=2048, Zipf(1.1)
   expert popularity.
+* Config 3 (Mixtral-8x7B layer, bf16): MoeLayerPlan at T=8192, H=4096, I=14336, 8 experts, top-2, against an fp32
+  torch chain of the experts and the combine (the oracle's bf16 GEMM is too slow at this size; routing, counts
+  and the dispatched rows are still checked against the oracle).
 
 The oracle runs the reference's chain on the same inputs: route (R0), layout and count exchange
 (dispatch_layout.h:112-161, notify_dispatch.h:340-412), fp8 dispatch (Q1/D3), GMM1 + SwiGLU + fp8 requant of
@@ -127,3 +130,39 @@ def test_layer_config4_fp8_matches_oracle_chain(ops, weights):
     assert np.array_equal(u8(plan.expand_x[:M]), ex), "fp8 codes differ from the oracle"
     assert np.array_equal(plan.scales[:M].cpu().numpy(), xs), "fp8 block scales differ from the oracle"
     assert relerr(out.cpu().float(), ref) < 5e-2
+
+
+def test_layer_config3_bf16_matches_fp32_reference(ops):
+    # config 3 at its own shape (Mixtral-8x7B: T=8192, H=4096, I=14336, 8 experts, top-2, bf16): MoeLayerPlan
+    # against an fp32 torch chain on the same routing (bf16 rounding of h and of the expert outputs, as the
+    # layer stores them), 2e-2 max-norm; ids, counts and the dispatched rows checked exactly against the oracle
+    import bench
+    from umdk_amd.plan import MoeLayerPlan
+    T, H3, E3, K3, I3 = 8192, 4096, 8, 2, 14336
+    print(f"config 3 bf16 layer T={T} H={H3} I={I3} E={E3} K={K3}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, H3, generator=g).bfloat16().cuda()
+    logits = torch.randn(T, E3, generator=g).cuda()
+    w1, _, w2, _ = bench.make_weights(E3, H3, I3, "bf16", torch.device("cuda"), 0)
+    plan = MoeLayerPlan(T, H3, E3, K3, E3, I3, dtype="bf16", device="cuda")
+    out = plan.forward(x, logits, None, w1, None, w2, None).clone()
+    torch.cuda.synchronize()
+    ridx, rw = orc.route(logits.cpu().numpy(), None, K3)
+    assert np.array_equal(plan.topk_idx.cpu().numpy(), ridx)
+    _, nte, _, sti = orc.dispatch_layout(ridx.astype(np.int64), E3, 1)
+    assert np.array_equal(plan.recv_tokens_per_expert[:E3].cpu().numpy(), nte.astype(np.int64))
+    so, _, _, _ = orc.notify_dispatch(nte)
+    ex, _, eidx = orc.dispatch(b16(x), ridx, so, sti, E3, orc.QUANT_NONE)
+    M = int(nte.sum())
+    assert np.array_equal(b16(plan.expand_x[:M]), ex)
+    # fp32 reference of the experts and the combine on the GPU's own gates
+    ids = plan.topk_idx.long()
+    wts = plan.topk_w
+    ref = torch.zeros(T, H3, device="cuda")
+    for e in range(E3):
+        tok, kk = (ids == e).nonzero(as_tuple=True)
+        gu = x[tok].float() @ w1[e].float().T
+        h = (gu[:, :I3] / (1 + torch.exp(-gu[:, :I3])) * gu[:, I3:]).bfloat16().float()
+        y = (h @ w2[e].float().T).bfloat16().float()
+        ref.index_add_(0, tok, y * wts[tok, kk].unsqueeze(1))
+    assert relerr(out.float(), ref) < 2e-2
