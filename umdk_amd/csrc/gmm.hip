@@ -109,23 +109,36 @@ __device__ void build_group_table(const int64_t *__restrict__ group_list, int L,
             rsum += c;
         }
     }
-    scratch[tid] = tsum;
-    scratch[GTHREADS + tid] = rsum;
-    __syncthreads();
-    if (tid == 0) {
-        int a = 0, b = 0;
-        for (int i = 0; i < GTHREADS; ++i) {
-            const int x = scratch[i], y = scratch[GTHREADS + i];
-            scratch[i] = a;
-            scratch[GTHREADS + i] = b;
-            a += x;
-            b += y;
+    // exclusive scan: within each wave by lane shuffles, then over the waves' totals
+    constexpr int NWV = GTHREADS / 64;
+    const int lane = tid & 63, wv = tid >> 6;
+    int ti = tsum, ri = rsum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int tu = __shfl_up(ti, d, 64), ru = __shfl_up(ri, d, 64);
+        if (lane >= d) {
+            ti += tu;
+            ri += ru;
         }
-        gt.tile_prefix[L] = a;
-        gt.row_off[L] = b;
+    }
+    if (lane == 63) {
+        scratch[wv] = ti;
+        scratch[NWV + wv] = ri;
     }
     __syncthreads();
-    int ta = scratch[tid], ra = scratch[GTHREADS + tid];
+    int ta = ti - tsum, ra = ri - rsum, at = 0, ar = 0;
+#pragma unroll
+    for (int v = 0; v < NWV; ++v) {
+        const int x = scratch[v], y = scratch[NWV + v];
+        ta += v < wv ? x : 0;
+        ra += v < wv ? y : 0;
+        at += x;
+        ar += y;
+    }
+    if (tid == 0) {
+        gt.tile_prefix[L] = at;
+        gt.row_off[L] = ar;
+    }
     for (int q = 0; q < per; ++q) {
         const int e = tid * per + q;
         if (e < L) {
@@ -197,7 +210,7 @@ __device__ __forceinline__ void lds_sync()
 // Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
 // (first < 0: balanced placement, see below), preceded by a run of rn tiles rs, rs + rstride, ... (an
 // increasing sequence: the first index past the class's tiles ends it).
-template <int DT, int EPI, int BM>
+template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM)>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first, int rs = 0, int rn = 0,
                                          int rstride = 1)
 {
@@ -326,9 +339,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
             dma16(p.A + c.ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
         } else if (q < A_LOADS + B_LOADS) {
             const int i = q - A_LOADS;
-            // decode tiles: the weights are a stream read once, fetched nontemporally (measured on the
-            // config-5 decode step: 244 vs 274 us)
-            if constexpr (BM <= CAM_GMM_NT_MAXBM)
+            // decode tiles and the light experts' tiles of a skewed prefill launch (NTW): the weights are a
+            // stream read about once, fetched nontemporally (measured: the config-5 decode step 244 vs
+            // 274 us, config 4's GMM1 216 vs 222 us)
+            if constexpr (NTW)
                 dma16_nt(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
             else
                 dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
@@ -861,7 +875,8 @@ constexpr int G_HEAVY_ROWS = 384;
 // 256-row tiles first, then the rest 128-row tiles -- one launch, the longest tiles first, the tile
 // sequence of each block continuing round-robin from the first class into the second.  A layer whose
 // load is skewed (a few experts with a thousand rows, many with a handful) gets tall tiles where they
-// halve the operand traffic and short ones where a tall tile would multiply padding.
+// halve the operand traffic and short ones where a tall tile would multiply padding.  The light experts'
+// (at most three M-tiles each) weights are fetched nontemporally.
 template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
 {
     // the first bytes of the dynamic LDS serve as the reduction slot before the tile body starts
@@ -916,7 +931,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
             free_all += fx;
         }
         const bool is_free = slot >= len;
-        gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
+        gmm_body<DT, EPI, 128, true>(p, 1, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
                                is_free ? (free_before + slot - len) * run : 0, is_free ? run : 0);
         return;
     }
@@ -924,7 +939,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
         __syncthreads();  // every wave is done with the first class's ring and table
     }
-    gmm_body<DT, EPI, 128>(p, 1, G_HEAVY_ROWS, n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1);
+    gmm_body<DT, EPI, 128, true>(p, 1, G_HEAVY_ROWS, n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1);
 }
 
 template <int BM> constexpr size_t lds_bytes()
