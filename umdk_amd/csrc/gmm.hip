@@ -61,23 +61,25 @@ constexpr int GBN = 256, GKB = 128;  // tile W-rows, bytes per row per k-step
 constexpr int GMAX_THREADS = 512;    // block size of the largest tile
 constexpr int G_MAX_L = 512;
 
-// Tile shapes (BM rows x 256 W rows, 128-byte k-steps):
+// Tile shapes (BM rows x BN W rows, 128-byte k-steps):
 //   BM = 256: 8 waves, 2 x 4 of 128 x 64, 2-stage ring -- half the L2->LDS bytes per FLOP of the
 //             128-row tile, for compute-bound prefill;
 //   BM = 128: 8 waves, 2 x 4 of 64 x 64, 3-stage ring;
 //   BM = 32:  4 waves, 1 x 4 of 32 x 64, 4-stage ring (decode: a handful of rows per expert, the k-loop
-//             is a weight stream and the extra stage keeps more of it in flight).
-template <int BM_> struct Tile {
-    static constexpr int BM = BM_;
+//             is a weight stream and the extra stage keeps more of it in flight);
+//   BM = 32, BN = 128: 4 waves of 32 x 32, 6-stage ring (the same bytes in flight) -- the decode GEMM
+//             without SwiGLU, whose tiles then divide evenly over the CUs.
+template <int BM_, int BN_ = GBN> struct Tile {
+    static constexpr int BM = BM_, BN = BN_;
     static constexpr int NWAVES = BM >= 128 ? 8 : 4;
     static constexpr int THREADS = 64 * NWAVES;
     static constexpr int WAVES_M = BM >= 128 ? 2 : 1;
     static constexpr int WAVES_N = NWAVES / WAVES_M;
-    static constexpr int WM = BM / WAVES_M, WN = GBN / WAVES_N;  // wave tile
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
     static constexpr int IF = WM / 16, JF = WN / 16;              // MFMA fragments per wave
-    static constexpr int STAGES = BM >= 256 ? 2 : BM >= 128 ? 3 : 4;
+    static constexpr int STAGES = BM >= 256 ? 2 : BM >= 128 ? 3 : BN >= 256 ? 4 : 6;
     static constexpr int A_BYTES = BM * GKB;
-    static constexpr int B_BYTES = GBN * GKB;
+    static constexpr int B_BYTES = BN * GKB;
     static constexpr int S_ROWS = WM > 64 ? WM : 64;  // activation-scale rows a wave DMAs (64 per instruction)
     static constexpr int S_DMAS = S_ROWS / 64;
     static constexpr int S_BYTES = NWAVES * S_ROWS * 4;  // per-wave copies of its rows' activation scales
@@ -85,6 +87,13 @@ template <int BM_> struct Tile {
     static constexpr int A_LOADS = A_BYTES / 1024 / NWAVES;  // DMA instructions per wave per stage (1 KiB each)
     static constexpr int B_LOADS = B_BYTES / 1024 / NWAVES;
 };
+
+// W rows per tile: 256, except the decode tile (BM = 32) of the plain GEMM (a SwiGLU tile holds the gate and
+// up rows of one 128-column scale block of h)
+#ifndef CAM_GMM_SMALL_PLAIN_BN
+#define CAM_GMM_SMALL_PLAIN_BN 128
+#endif
+constexpr int small_bn(int bm, int epi) { return bm == 32 && epi == 0 ? CAM_GMM_SMALL_PLAIN_BN : GBN; }
 
 struct GroupTable {
     int tile_prefix[G_MAX_L + 1];  // exclusive prefix of M-tiles per expert
@@ -214,7 +223,8 @@ template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM)>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first, int rs = 0, int rn = 0,
                                          int rstride = 1)
 {
-    using TC = Tile<BM>;
+    using TC = Tile<BM, small_bn(BM, EPI)>;
+    constexpr int TBN = TC::BN;
     constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
     constexpr int GBM = TC::BM, WM = TC::WM, WN = TC::WN, IF = TC::IF, JF = TC::JF;
     constexpr int GSTAGES = TC::STAGES, STAGE_BYTES = TC::STAGE_BYTES;
@@ -237,7 +247,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
     const uint32_t kbytes = (uint32_t)p.K * esz;  // bytes per row
     const int nk = (int)(kbytes / GKB);
     const int half_n = p.N / 2;                    // I for SwiGLU
-    const int ntn = SWIGLU ? half_n / 128 : p.N / GBN;
+    const int ntn = SWIGLU ? half_n / 128 : p.N / TBN;
     const int total = __builtin_amdgcn_readfirstlane(gt->tile_prefix[p.L]) * ntn;
 
     // first < 0: this launch has one tile class, so balance it: with R = ceil(total / grid) rounds, only
@@ -268,7 +278,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         const float *wsb;  // this expert's weight scales (fp8 block or int8 per-channel), or null
         uint32_t ga[A_LOADS], gb[B_LOADS], gs[TC::S_DMAS];
         int wsg, wsu;  // fp8: weight-scale row offsets (gate / up n-blocks, or the wave's column block)
-        bool active;   // some row of this wave lies inside the segment
+        int active;    // some row of this wave lies inside the segment (an int: a bool tail makes struct copies go through scratch)
     };
     auto setup = [&](int tile, Ctx &c) {
         int lo = 0, hi = p.L - 1;
@@ -293,13 +303,16 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
         c.seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
         c.row0 = seg0 + mt * GBM;
-        c.n0 = SWIGLU ? nt * 128 : nt * GBN;  // first h-column (SwiGLU) or W row (plain)
+        c.n0 = SWIGLU ? nt * 128 : nt * TBN;  // first h-column (SwiGLU) or W row (plain)
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
         // DMA and meets every barrier): a tile of a short segment costs little more than its weights
         c.active = c.row0 + wm * WM < c.seg1;
-        if (p.Wl) {  // separated weights: one allocation per expert
-            c.wbase = p.Wl[e];
-            c.wsb = p.Wsl ? p.Wsl[e] : nullptr;
+        if (p.Wl) {  // separated weights: one allocation per expert, pointers read by scalar loads (a vector
+                     // load here would make the tile switch wait for every DMA in flight)
+            c.wbase = reinterpret_cast<const uint8_t *>(
+                ((const __attribute__((address_space(4))) uint64_t *)p.Wl)[e]);
+            c.wsb = p.Wsl ? reinterpret_cast<const float *>(((const __attribute__((address_space(4))) uint64_t *)p.Wsl)[e])
+                          : nullptr;
         } else {
             c.wbase = p.W + (size_t)e * p.N * kbytes;
             c.wsb = !p.Ws ? nullptr : p.Ws + (INT8 ? (size_t)e * p.N : (size_t)e * (p.N / 128) * nk);
@@ -627,10 +640,13 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
             auto stage_ptr = [&](int ks) { return smem + slot(ks) * STAGE_BYTES; };
             // DMA instruction q of the current tile's k-step ksx (ksx may run past the end)
             auto dma_ks = [&](int ksx, int q) {
-                const bool in = ksx < nk;
-                const Ctx &c = (!in && chain) ? nxt : cur;
-                const int kc = in ? ksx : (chain ? ksx - nk : nk - 1);
-                dma_one(c, kc, slot(ksx), q);
+                // a uniform branch between two direct calls: selecting the context by reference would
+                // place one of them in scratch memory, and every reload from there waits for the whole
+                // DMA ring (vmcnt(0))
+                if (ksx >= nk && chain)
+                    dma_one(nxt, ksx - nk, slot(ksx), q);
+                else
+                    dma_one(cur, min(ksx, nk - 1), slot(ksx), q);
             };
             // the DMAs that follow MFMA n of NMF in a phase: spread evenly, so that a wave stalled on
             // a DMA issue still has MFMAs in the pipe
@@ -942,11 +958,12 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     gmm_body<DT, EPI, 128, true>(p, 1, G_HEAVY_ROWS, n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1);
 }
 
-template <int BM> constexpr size_t lds_bytes()
+template <int BM, int BN = GBN> constexpr size_t lds_bytes()
 {
-    return Tile<BM>::STAGES * Tile<BM>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int);
+    return Tile<BM, BN>::STAGES * Tile<BM, BN>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int);
 }
-static_assert(lds_bytes<32>() <= 163840 && lds_bytes<128>() <= 163840 && lds_bytes<256>() <= 163840,
+static_assert(lds_bytes<32>() <= 163840 && lds_bytes<32, 128>() <= 163840 && lds_bytes<128>() <= 163840 &&
+                  lds_bytes<256>() <= 163840,
               "LDS budget of a gfx950 workgroup");
 
 
@@ -1000,7 +1017,7 @@ template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s
     const int grid = (num_cus(dev) + 7) / 8 * 8;
     if (a.M <= 48 * a.L) {
         static std::atomic<bool> done[G_MAX_DEVICES];
-        const size_t lds = lds_bytes<32>();
+        const size_t lds = lds_bytes<32, small_bn(32, EPI)>();
         hipError_t e = set_lds(gmm_kernel_small<DT, EPI>, lds, dev, done);
         if (e != hipSuccess)
             return e;
