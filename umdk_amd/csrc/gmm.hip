@@ -8,7 +8,7 @@
 //   [L, N/128, K/128]).
 //   GMM1+SwiGLU (EPI_SWIGLU_*): N = 2I, rows [0,I) of W are the gate and
 //     [I,2I) the up projection (block_epilogue_per_token_dequant_swiglu.h:256-286:
-//     silu on the left half); h = silu(g) * u, silu(g) = g / (1 + exp(-g)),
+//     silu on the left half); h = silu(g) * u, silu(g) = g / (1 + exp(-g)) (hardware exp and reciprocal),
 //     stored as bf16, or requantised to fp8 per 1x128 block of h exactly like
 //     the dispatch quantiser (post_swiglu_dynamic_quant.h:164-231 requantises
 //     per token in int8).
@@ -397,7 +397,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const float g = acc[i][j][q], u = acc[i][j + HF][q];
-                        h[i][j][q] = g / (1.0f + expf(-g)) * u;
+                        // silu(g) = g / (1 + exp(-g)) with the hardware exp and reciprocal (about 1 ulp
+                        // each; measured: the decode step 1 us and the M = 65536 fp8 GMM1 4% faster than
+                        // the correctly rounded division)
+                        h[i][j][q] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     }
             if constexpr (EPI == EPI_SWIGLU_F32AMAX) {
                 // fp32 h and this wave's partial row maximum of |h| (its 32 h-columns), one slot per wave and
