@@ -633,8 +633,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         while (true) {
             const int ntile = seq(++kt);
             const bool has_next = ntile < total;
-            // (int8: the dequantisation's vector loads would wait for the next tile's DMAs, so no chaining)
-            const bool chain = !INT8 && has_next && nk >= GSTAGES;
+            // (int8 chains too: its dequantisation's vector loads then wait for the next tile's first DMAs,
+            // which land meanwhile -- measured 8 us faster on the int8 decode step than draining first)
+            const bool chain = has_next && nk >= GSTAGES;
             if (has_next)
                 setup(ntile, nxt);
             else
