@@ -208,6 +208,41 @@ def graph_time(fn, n, warmup, stream):
     return a.elapsed_time(b) / n
 
 
+def cold_time(fn, n, stream, flush_bytes=512 << 20):
+    """(median ms with cold caches, median ms without a flush) of fn over n single-step graph replays, each
+    timed by its own pair of HIP events.  The cold runs read a 512 MiB buffer outside the timed region first
+    (the reference's timing method flushes the L2 and the 256 MB MALL between timed runs; reading leaves only
+    clean lines, so no write-back of the flush lands in the timed step)."""
+    flush = torch.ones(flush_bytes // 4, dtype=torch.int32, device=stream.device)
+    sink = torch.empty((), dtype=torch.int64, device=stream.device)
+    side = torch.cuda.Stream(device=stream.device)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        fn()
+        fn()
+    stream.wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        fn()
+    stream.wait_stream(side)
+    out = []
+    for cold in (True, False):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        with torch.cuda.stream(stream):
+            graph.replay()
+            for a, b in ev:
+                if cold:
+                    torch.sum(flush, dim=0, out=sink)
+                a.record(stream)
+                graph.replay()
+                b.record(stream)
+        torch.cuda.synchronize()
+        t = sorted(a.elapsed_time(b) for a, b in ev)
+        out.append(t[len(t) // 2])
+    del graph, flush
+    return out[0], out[1]
+
+
 def zipf_bias(E, s, seed):
     """log-popularity bias: expert popularity ~ 1/rank^s over a seeded permutation of the ids"""
     g = torch.Generator().manual_seed(seed + 17)
@@ -540,6 +575,7 @@ def main():
     c_ms = graph_time(lambda: plan.combine_step(y), n, args.warmup, stream)
     ms_ops = graph_time(step_ops, n, args.warmup, stream)
     d_ms = graph_time(lambda: plan.dispatch(x), n, args.warmup, stream)      # the dispatch launch alone
+    cold_ms, single_ms = cold_time(step, 20, stream)
     c_ops_ms = graph_time(lambda: plan.combine(y), n, args.warmup, stream)   # scatter + gather
     db, cb = dispatch_bytes(T, H, K), combine_bytes(T, H, K)
     comb_gbps = cb / (c_ms * 1e-3) / 1e9
@@ -571,6 +607,11 @@ def main():
         "step_launches": "camhipMoePrefillDispatch (route+histogram, scan+count exchange, dispatch) + "
                          "camhipMoePrefillCombine (gather)",
         "dispatch_step_ms": ds_ms,
+        "cold_caches": {"ms_per_step_median": cold_ms, "tokens_per_s": T / (cold_ms * 1e-3),
+                        "same_without_flush_ms": single_ms,
+                        "method": "one step per graph replay, 20 replays, each after reading 512 MiB (L2 and MALL "
+                                  "flushed), per-replay HIP events, median; the same replays without the flush "
+                                  "beside it"},
         "dispatch": {"ms": d_ms, "GBps": disp_gbps, "frac": disp_gbps / HBM_PEAK_GBPS, "algorithmic_bytes": db,
                      "timed_in": "the reference-op chain (the dispatch launch alone)"},
         "combine": {"ms": c_ms, "GBps": comb_gbps, "frac": comb_gbps / HBM_PEAK_GBPS},
