@@ -65,6 +65,11 @@ MAXL_A[0], MAXL_A[255], MAXL_A[511] = 5, 70, 3
 MAXL_B = [0] * 512
 MAXL_B[3], MAXL_B[500], MAXL_B[511] = 25000, 40, 1
 SMALL += [(MAXL_A, 512, 128), (MAXL_B, 256, 128)]
+# decode-sized rows over 32 experts (0-8 each, 128 rows: the 32-row kernel) with 512 tiles per GEMM, two per
+# block or more: the tile switch (the next tile's prefetch issued during the current one) and the 32 x 128
+# tiles of the plain GEMM, against the oracle
+DECODE = [(e * 7) % 9 for e in range(32)]
+SMALL += [(DECODE, 2048, 2048)]
 
 
 @pytest.mark.parametrize("counts,H,I", SMALL)

@@ -62,8 +62,10 @@ def check_requant(hq, hs, q_ref, s_ref):
     assert (d > 0).mean() <= 1e-3, f"{(d > 0).mean():.2e} of the codes moved"
 
 
-# rows per expert, H (k of GMM1), I; the first two take the 32-row tile, the others the 8-wave kernel
-CASES = [([3, 40, 0, 7], 1024, 256), ([1], 512, 128), ([5, 0, 300], 256, 256), ([17, 256, 255, 1, 0, 9], 512, 128)]
+# rows per expert, H (k of GMM1), I; the first two and the last take the 32-row tile, the others the 8-wave
+# kernel; the last has several tiles per block (the int8 tiles chain the next tile's prefetch)
+CASES = [([3, 40, 0, 7], 1024, 256), ([1], 512, 128), ([5, 0, 300], 256, 256), ([17, 256, 255, 1, 0, 9], 512, 128),
+         ([(e * 7) % 9 for e in range(32)], 2048, 2048)]
 
 
 @pytest.mark.parametrize("counts,H,I", CASES)
