@@ -445,7 +445,11 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                 }
             } else {
                 // fp8 1x128 requant: the tile's 128 h-columns of a row are one scale block,
-                // split over the column waves; exchange partial amax through LDS
+                // split over the column waves; exchange partial amax through LDS.  The lane's row and
+                // column offsets are recomputed here from the lane id (mbcnt): values kept from the kernel's
+                // start are spilled by the k-loop, and each reload would wait on every store issued before it
+                const int lid = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+                const int l16 = lid & 15, lg = lid >> 4;
                 float *red = reinterpret_cast<float *>(scratch);  // [WAVES_N][GBM]
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
@@ -461,15 +465,22 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                         red[wn * GBM + wm * WM + i * 16 + l16] = mx;
                 }
                 lds_sync();
+                // every row's block maximum first, then all the stores back to back: a register reload
+                // between two rows' stores would wait for the earlier stores to complete (vmcnt counts both)
+                float amx[IF];
 #pragma unroll
                 for (int i = 0; i < IF; ++i) {
                     const int r = wm * WM + i * 16 + l16;
-                    const int m = row0 + r;
                     float amax = 1e-4f;
 #pragma unroll
                     for (int cc = 0; cc < TC::WAVES_N; ++cc)
                         amax = fmaxf(amax, red[cc * GBM + r]);
-                    const float inv = 448.0f / amax;
+                    amx[i] = amax;
+                }
+#pragma unroll
+                for (int i = 0; i < IF; ++i) {
+                    const int m = row0 + wm * WM + i * 16 + l16;
+                    const float inv = 448.0f / amx[i];
                     if (m < seg1) {
                         uint8_t *hrow = p.C + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
 #pragma unroll
@@ -477,7 +488,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                             *reinterpret_cast<uint32_t *>(hrow + 16 * j) = f32x4_to_e4m3(
                                 h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv, h[i][j][3] * inv);
                         if (wn == 0 && lg == 0)
-                            p.Cs[(size_t)(n0 / 128) * p.M + m] = amax / 448.0f;  // k-major h scales
+                            p.Cs[(size_t)(n0 / 128) * p.M + m] = amx[i] / 448.0f;  // k-major h scales
                     }
                 }
                 lds_sync();  // red is reused by the next tile
