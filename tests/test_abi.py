@@ -99,6 +99,16 @@ def test_route_limits(L):
     assert L.camhipMoeRoute(None, 0, None, None) == 161002  # NULL executor
 
 
+def test_reference_import_name():
+    # the reference's call sites import the extension by its module name, then use torch.ops.umdk_cam_op_lib.*
+    # (test_fused_deep_moe.py:24, 219); both work unchanged
+    import torch
+    import umdk_cam_op_lib
+    for name in ("fused_deep_moe", "get_dispatch_layout", "moe_dispatch_prefill", "moe_combine_prefill"):
+        assert callable(getattr(umdk_cam_op_lib, name))
+        assert hasattr(torch.ops.umdk_cam_op_lib, name)
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     import umdk_amd  # noqa: F401
