@@ -503,15 +503,44 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                 acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
-    if constexpr (FP8 && BM >= 256) {
-        // 256-row fp8 tile (8 waves of 128 x 64): half the L2->LDS bytes per FLOP of the 128-row
+    // int8: per-channel x per-token dequantisation of the exact int32 sums:
+    // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
+    auto dequant_int8 = [&](const Ctx &cur) {
+        if constexpr (INT8) {
+            const float *wsr = cur.wsb;
+#pragma unroll
+            for (int j = 0; j < JF; ++j) {
+                int c0;
+                if (SWIGLU) {
+                    const int jj = j % (JF / 2);
+                    c0 = cur.n0 + (WN / 2) * wn + 16 * jj + 4 * lg + (j >= JF / 2 ? half_n : 0);
+                } else {
+                    c0 = cur.n0 + wn * WN + 16 * j + 4 * lg;
+                }
+                const f32x4 wv = *reinterpret_cast<const f32x4 *>(wsr + c0);
+#pragma unroll
+                for (int i = 0; i < IF; ++i) {
+                    const float xs = p.As[min(cur.row0 + wm * WM + i * 16 + l16, p.M - 1)];
+                    const i32x4 iv = __builtin_bit_cast(i32x4, acc[i][j]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[i][j][q] = ((float)iv[q] * wv[q]) * xs;
+                }
+            }
+        }
+    };
+
+    if constexpr (BM >= 256) {
+        // 256-row tile (8 waves of 128 x 64; fp8, bf16 or int8): half the L2->LDS bytes per FLOP of the 128-row
         // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
         // W fragments of a k-step read once after the barrier, the A fragments streamed AHEAD rows
         // in front of the MFMAs that use them (the other wave on the SIMD covers the W read), the
         // next k-step's A bands issued during the first half of this k-step's MFMAs and the W bands
         // of the k-step after it from the middle on (a second barrier frees the W slot as soon as the
         // fragments are in registers).  Tiles do not overlap: each starts with its own first DMA and
-        // drains at its end.
+        // drains at its end.  bf16 and int8 run the same loop with two chained K-half MFMAs per fragment pair
+        // and no block scaling (measured against the generic two-stage loop, which waits for the whole ring
+        // at every k-step: config 3's bf16 GEMMs 1.16 -> 1.27 PFLOPS, the int8 M-sweep's GMM1 +11%).
         static_assert(GSTAGES == 2, "two-stage ring");
         constexpr int AHEAD = 2;
         for (int kt = 0, tile = seq(0); tile < total; tile = seq(++kt)) {
@@ -554,7 +583,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                         const u32x4 v1 = *reinterpret_cast<const u32x4 *>(la + swz(i * 16 + l16, 4 + lg));
                         a[i] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                      (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
-                        sa[i] = sst[i * 16 + l16];
+                        if constexpr (FP8)
+                            sa[i] = sst[i * 16 + l16];
                     };
 #pragma unroll
                     for (int j = 0; j < JF; ++j) {
@@ -563,7 +593,11 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                         b[j] = i32x8{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
                                      (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
                     }
-                    const float sg = sload(c.wsb, c.wsg + ks), su = SWIGLU ? sload(c.wsb, c.wsu + ks) : sg;
+                    float sg = 0.0f, su = 0.0f;
+                    if constexpr (FP8) {
+                        sg = sload(c.wsb, c.wsg + ks);
+                        su = SWIGLU ? sload(c.wsb, c.wsu + ks) : sg;
+                    }
                     const int kn = min(ks + 1, nk - 1);  // past the end: reload the last k-step
 #pragma unroll
                     for (int i = 0; i < AHEAD; ++i)
@@ -572,11 +606,27 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                     for (int i = 0; i < IF; ++i) {
                         if (i + AHEAD < IF)
                             rd_a(i + AHEAD);
-                        const float sgi = sa[i] * sg, sui = sa[i] * su;
+                        const float sgi = FP8 ? sa[i] * sg : 0.0f, sui = FP8 ? sa[i] * su : 0.0f;
                         const int pi = i == 0 ? IF - 1 : i - 1;  // row of the pending results
 #pragma unroll
                         for (int j = 0; j < JF; ++j) {
-                            if constexpr (decltype(act)::value) {
+                            if constexpr (decltype(act)::value && !FP8) {
+                                // bf16 / int8: the lane's two 16-byte chunks are the k-step's two K halves
+                                // (32 bf16 or 64 int8 elements each); int8 accumulates exact int32 sums
+                                const i32x4 b0 = {b[j][0], b[j][1], b[j][2], b[j][3]}, b1 = {b[j][4], b[j][5], b[j][6], b[j][7]};
+                                const i32x4 a0 = {a[i][0], a[i][1], a[i][2], a[i][3]}, a1 = {a[i][4], a[i][5], a[i][6], a[i][7]};
+                                if constexpr (INT8) {
+                                    i32x4 t = __builtin_bit_cast(i32x4, acc[i][j]);
+                                    t = __builtin_amdgcn_mfma_i32_16x16x64_i8(b0, a0, t, 0, 0, 0);
+                                    t = __builtin_amdgcn_mfma_i32_16x16x64_i8(b1, a1, t, 0, 0, 0);
+                                    acc[i][j] = __builtin_bit_cast(f32x4, t);
+                                } else {
+                                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                        __builtin_bit_cast(bf16x8, b0), __builtin_bit_cast(bf16x8, a0), acc[i][j], 0, 0, 0);
+                                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                        __builtin_bit_cast(bf16x8, b1), __builtin_bit_cast(bf16x8, a1), acc[i][j], 0, 0, 0);
+                                }
+                            } else if constexpr (decltype(act)::value) {
                                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                                 const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], z, 0,
                                                                                                  0, 0, 127, 0, 127);
@@ -604,8 +654,12 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                                 for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
                                     dma_one(c, min(ks + 2, nk - 1), ks & 1, q);
                             }
-                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                            if constexpr (FP8) {
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+                            } else {
+                                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+                            }
                             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a DMA, where one follows
                         }
                     }
@@ -615,13 +669,16 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                 kloop(std::true_type{});
             else
                 kloop(std::false_type{});
+            if constexpr (FP8) {
 #pragma unroll
-            for (int j = 0; j < JF; ++j)  // the last row's pending results
+                for (int j = 0; j < JF; ++j)  // the last row's pending results
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    acc[IF - 1][j][q] += pend[j][q] * ps[j];
+                    for (int q = 0; q < 4; ++q)
+                        acc[IF - 1][j][q] += pend[j][q] * ps[j];
+            }
             wait_vmcnt<0>();  // the tail's reload has landed before the next tile reuses the ring
             bar();
+            dequant_int8(c);
             epilogue(c);
         }
         return;
@@ -843,30 +900,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                     kloop(std::false_type{});
             }
 
-            if constexpr (INT8) {
-                // per-channel x per-token dequantisation of the exact int32 sums:
-                // v = ((float)acc * w_scale[n]) * x_scale[m]  (block_epilogue_per_token_dequant*.h)
-                const float *wsr = cur.wsb;
-#pragma unroll
-                for (int j = 0; j < JF; ++j) {
-                    int c0;
-                    if (SWIGLU) {
-                        const int jj = j % (JF / 2);
-                        c0 = cur.n0 + (WN / 2) * wn + 16 * jj + 4 * lg + (j >= JF / 2 ? half_n : 0);
-                    } else {
-                        c0 = cur.n0 + wn * WN + 16 * j + 4 * lg;
-                    }
-                    const f32x4 wv = *reinterpret_cast<const f32x4 *>(wsr + c0);
-#pragma unroll
-                    for (int i = 0; i < IF; ++i) {
-                        const float xs = p.As[min(cur.row0 + wm * WM + i * 16 + l16, p.M - 1)];
-                        const i32x4 iv = __builtin_bit_cast(i32x4, acc[i][j]);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            acc[i][j][q] = ((float)iv[q] * wv[q]) * xs;
-                    }
-                }
-            }
+            dequant_int8(cur);
             if (!chain) {
                 wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
                 bar();
