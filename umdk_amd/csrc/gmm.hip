@@ -41,6 +41,7 @@
 //     groups of 8 M-tiles x all N-tiles (M fastest), remapped so that the
 //     blocks of one XCD take consecutive tiles: they share A and W tiles in
 //     that XCD's L2.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -320,7 +321,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
             const int r = (i * NW + w) * 8 + band_row;  // tile row 0..GBM-1
-            c.ga[i] = (uint32_t)min(c.row0 + r, p.M - 1) * kbytes + chunk_off(r);
+            c.ga[i] = (uint32_t)min(c.row0 + r, c.seg1 - 1) * kbytes + chunk_off(r);
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
@@ -340,7 +341,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         // fp8: this wave's activation-scale rows (the WM rows of its row block wm, 64 per DMA)
 #pragma unroll
         for (int d = 0; d < TC::S_DMAS; ++d)
-            c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, p.M - 1);  // k-major: + kc * M
+            c.gs[d] = (uint32_t)min(c.row0 + wm * WM + d * 64 + lane, c.seg1 - 1);  // k-major: + kc * M
         c.wsg = ((SWIGLU ? c.n0 : c.n0 + wn * WN) / 128) * nk;
         c.wsu = SWIGLU ? ((half_n + c.n0) / 128) * nk : c.wsg;
     };
@@ -935,10 +936,23 @@ template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_
 // expert (counts are on the device).  The choice is block-uniform and identical in every block.
 // Experts with at least this many rows take the 256-row tile (when the launch allows it).
 constexpr int G_HEAVY_ROWS = 384;
+// In a launch with heavy experts (fp8 and bf16), the experts with fewer rows than this take the 32-row tile on
+// four of the block's waves: their tiles are a weight stream, and that tile's four-stage ring keeps half as
+// many weight bytes again in flight per CU as the 128-row tile's three stages (measured on config 4's fp8
+// GMM1: such a tile streams its 1.8 MB in 46-58 us against 51-65 us, the GEMM 186 vs 193 us; the int8 GEMM
+// measured 1-2% slower and keeps the 128-row tile).
+#ifndef CAM_GMM_SMALL_ROWS
+#define CAM_GMM_SMALL_ROWS 64
+#endif
+constexpr int G_SMALL_ROWS = CAM_GMM_SMALL_ROWS;
+#ifndef CAM_GMM_RUN32
+#define CAM_GMM_RUN32 3
+#endif
 
 // Prefill: 8 waves.  With the 256-row tile allowed, the experts holding at least G_HEAVY_ROWS rows run
 // 256-row tiles first, then the rest 128-row tiles -- one launch, the longest tiles first, the tile
-// sequence of each block continuing round-robin from the first class into the second.  A layer whose
+// sequence of each block continuing round-robin from the first class into the second, and (fp8, bf16) from
+// there into a third, the experts with fewer than G_SMALL_ROWS rows on 32-row tiles.  A layer whose
 // load is skewed (a few experts with a thousand rows, many with a handful) gets tall tiles where they
 // halve the operand traffic and short ones where a tall tile would multiply padding.  The light experts'
 // (at most three M-tiles each) weights are fetched nontemporally.
@@ -955,6 +969,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, -1);
         return;
     }
+    constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
     int *red = reinterpret_cast<int *>(smem);
     if (threadIdx.x == 0)
         red[0] = 0;
@@ -996,15 +1011,31 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
             free_all += fx;
         }
         const bool is_free = slot >= len;
-        gmm_body<DT, EPI, 128, true>(p, 1, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
-                               is_free ? (free_before + slot - len) * run : 0, is_free ? run : 0);
+        const int fpos = free_before + slot - len;  // the block's rank among the free blocks
+        gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
+                                     is_free ? fpos * run : 0, is_free ? run : 0);
+        if constexpr (SMALL > 1) {
+            __syncthreads();
+            if (threadIdx.x >= Tile<32>::THREADS)
+                return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
+            constexpr int run32 = CAM_GMM_RUN32;
+            gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * free_all + (int)blockIdx.x,
+                                        is_free ? fpos * run32 : 0, is_free ? run32 : 0);
+        }
         return;
     }
     if (n_heavy > 0) {
         gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
         __syncthreads();  // every wave is done with the first class's ring and table
     }
-    gmm_body<DT, EPI, 128, true>(p, 1, G_HEAVY_ROWS, n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1);
+    const int lpos = n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1;
+    gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, lpos);
+    if constexpr (SMALL > 1) {
+        __syncthreads();
+        if (threadIdx.x >= Tile<32>::THREADS)
+            return;
+        gmm_body<DT, EPI, 32, true>(p, 1, SMALL, lpos);
+    }
 }
 
 template <int BM, int BN = GBN> constexpr size_t lds_bytes()
@@ -1075,7 +1106,7 @@ template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s
     }
     a.allow256 = a.M >= G_HEAVY_ROWS;  // some expert may reach the 256-row tile class
     static std::atomic<bool> done[G_MAX_DEVICES];
-    const size_t lds = lds_bytes<128>() > lds_bytes<256>() ? lds_bytes<128>() : lds_bytes<256>();
+    const size_t lds = std::max(std::max(lds_bytes<128>(), lds_bytes<256>()), lds_bytes<32>());
     hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, dev, done);
     if (e != hipSuccess)
         return e;
