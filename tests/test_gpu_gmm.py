@@ -234,8 +234,23 @@ def test_gmm_fp8_long_reduction(ops):
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
 def test_gmm_mixed_tile_heights_in_one_launch(ops, dtype):
-    # experts with >= 384 rows take 256-row tiles, the others 128-row tiles, in the same launch
-    _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383], 1024, 256, dtype, 7, 25)
+    # GMM1 at H = 4096 (>= 32 k-steps): experts with >= 384 rows take 256-row tiles, those with 64..383 rows
+    # 128-row tiles and those with fewer than 64 rows 32-row tiles on four waves, in the same launch (fewer
+    # heavy tiles than blocks: the heavy tiles split over the XCDs, the free blocks start the others)
+    _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383, 63, 64, 1], 4096, 256, dtype, 7, 25)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_mixed_tile_heights_many_heavy_tiles(ops, dtype):
+    # as above with at least as many heavy tiles as blocks (18 heavy M-tiles x 16 N-tiles): every block runs
+    # the heavy class first, then the 128- and 32-row classes round-robin
+    _ragged_vs_torch(ops, [2100, 40, 2100, 150, 3], 4096, 2048, dtype, 3, 27)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_gmm_mixed_tile_heights_short_reduction(ops, dtype):
+    # H = 1024 (fewer than 32 k-steps): every expert takes the 128-row tile, whatever its rows
+    _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383], 1024, 256, dtype, 7, 28)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
