@@ -54,6 +54,9 @@ namespace cam {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
+#ifndef CAM_GMM_MIN_NK256
+#define CAM_GMM_MIN_NK256 16
+#endif
 #ifndef CAM_GMM_NT_MAXBM
 #define CAM_GMM_NT_MAXBM 32  // tile heights up to this stream their weights nontemporally
 #endif
@@ -200,6 +203,29 @@ __device__ __forceinline__ void dma16_nt(const void *g, void *lds)
 __device__ __forceinline__ void dma4(const void *g, void *lds)
 {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
+}
+
+// The same DMAs through a buffer resource: the base sits in four SGPRs, the lane's 32-bit byte offset in one
+// VGPR and the k-step's offset in an SGPR, so a DMA needs no 64-bit address registers and no address
+// arithmetic per k-step.  Offsets are 32-bit (every operand here is under 4 GiB); the record count is
+// unbounded.
+#ifndef CAM_GMM_BUFDMA
+#define CAM_GMM_BUFDMA 1
+#endif
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
+}
+template <int BYTES, int AUX>
+__device__ __forceinline__ void bdma(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds)
+{
+    auto *l = (__attribute__((address_space(3))) void *)lds;
+    if constexpr (BYTES == 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, voff, soff, 0, 0);
+    else if constexpr (AUX == 2)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, voff, soff, 0, 2);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, voff, soff, 0, 0);
 }
 
 // scalar (SMEM) load of a block-uniform element of read-only data: it counts on lgkmcnt, not on the
@@ -349,6 +375,20 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
     // W bands, then (fp8) the activation scales
     auto dma_one = [&](const Ctx &c, int kc, int slot, int q) {
         uint8_t *st = smem + slot * STAGE_BYTES;
+        if constexpr (CAM_GMM_BUFDMA && BM >= 128) {  // (the decode tile measured 0.4 us slower per step this way)
+            if (q < A_LOADS) {
+                bdma<16, 0>(buf_rsrc(p.A), c.ga[q], (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
+            } else if (q < A_LOADS + B_LOADS) {
+                const int i = q - A_LOADS;
+                bdma<16, NTW ? 2 : 0>(buf_rsrc(c.wbase), c.gb[i], (uint32_t)kc * GKB,
+                                      st + A_BYTES + (i * NW + w) * 1024);
+            } else {
+                const int d = q - A_LOADS - B_LOADS;
+                bdma<4, 0>(buf_rsrc(p.As), c.gs[d] * 4u, (uint32_t)kc * (uint32_t)p.M * 4u,
+                           st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            }
+            return;
+        }
         if (q < A_LOADS) {
             dma16(p.A + c.ga[q] + (uint32_t)kc * GKB, st + (q * NW + w) * 1024);
         } else if (q < A_LOADS + B_LOADS) {
@@ -544,18 +584,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         // at every k-step: config 3's bf16 GEMMs 1.16 -> 1.27 PFLOPS, the int8 M-sweep's GMM1 +11%).
         static_assert(GSTAGES == 2, "two-stage ring");
         constexpr int AHEAD = 2;
-        for (int kt = 0, tile = seq(0); tile < total; tile = seq(++kt)) {
-            Ctx c;
-            setup(tile, c);
-            clear_acc();
-            f32x4 pend[JF];
-            float ps[JF];
-#pragma unroll
-            for (int j = 0; j < JF; ++j) {
-                pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-                ps[j] = 0.0f;
-            }
-            // the W bands of k-step 0, its A bands and scales, then the W bands of k-step 1
+        // a tile's first DMAs: the W bands of k-step 0, its A bands and scales, then the W bands of k-step 1
+        auto prime = [&](const Ctx &c) {
 #pragma unroll
             for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
                 dma_one(c, 0, 0, q);
@@ -566,6 +596,22 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
 #pragma unroll
             for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
                 dma_one(c, min(1, nk - 1), 1, q);
+        };
+        int kt = 0, tile = seq(0);
+        Ctx c;
+        if (tile < total) {
+            setup(tile, c);
+            prime(c);
+        }
+        while (tile < total) {
+            clear_acc();
+            f32x4 pend[JF];
+            float ps[JF];
+#pragma unroll
+            for (int j = 0; j < JF; ++j) {
+                pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ps[j] = 0.0f;
+            }
             auto kloop = [&](auto act) {
                 for (int ks = 0; ks < nk; ++ks) {
                     // k-step ks has landed (only the W bands of ks+1, issued last, may still be in flight);
@@ -681,6 +727,15 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
             bar();
             dequant_int8(c);
             epilogue(c);
+            // int8: the dequantisation's loads have landed before the next tile (otherwise the compiler,
+            // unsure of them, waits for every DMA in flight inside the k-loop)
+            if constexpr (INT8)
+                wait_vmcnt<0>();
+            tile = seq(++kt);
+            if (tile < total) {
+                setup(tile, c);
+                prime(c);
+            }
         }
         return;
     } else {
@@ -963,9 +1018,10 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int pos = xcd_position();
     // short reductions keep the 128-row tile: the 256-row tile's per-tile ring fill and drain would
-    // not amortise over fewer than 32 k-steps
+    // not amortise over fewer than 16 k-steps (at 16, GMM2 of DeepSeek-V3's shapes: the M = 65536 fp8 GMM2
+    // 1.71 vs 1.57 PFLOPS, int8 1.97 vs 1.67 POPS, config 4's fp8 GMM2 116 vs 122 us)
     const int nk = (int)((uint32_t)p.K * (DT == DT_BF16 ? 2 : 1) / GKB);
-    if (!p.allow256 || nk < 32) {
+    if (!p.allow256 || nk < CAM_GMM_MIN_NK256) {
         gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, -1);
         return;
     }
