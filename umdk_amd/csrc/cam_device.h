@@ -22,6 +22,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f)
     return u >> 16;
 }
 
+// Two fp32 -> two bf16 (round to nearest even) packed little-endian, by the hardware conversion
+// (v_cvt_pk_bf16_f32): one instruction for what f32_to_bf16 takes four for, the same bits for every
+// finite input.
+typedef __bf16 cam_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float cam_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((cam_f32x2{a, b}), cam_bf16x2));
+}
+
 // Unpack 8 bf16 held in a 16-byte vector into fp32.
 __device__ __forceinline__ void unpack_bf16x8(const u32x4 v, float *f)
 {

@@ -422,8 +422,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
 #pragma unroll
                 for (int j = 0; j < JF; ++j) {
                     u32x2 v;
-                    v[0] = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
-                    v[1] = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
+                    v[0] = f32x2_to_bf16x2(acc[i][j][0], acc[i][j][1]);
+                    v[1] = f32x2_to_bf16x2(acc[i][j][2], acc[i][j][3]);
                     *reinterpret_cast<u32x2 *>(crow + 16 * j) = v;
                 }
             }
@@ -479,8 +479,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
 #pragma unroll
                     for (int j = 0; j < HF; ++j) {
                         u32x2 v;
-                        v[0] = f32_to_bf16(h[i][j][0]) | (f32_to_bf16(h[i][j][1]) << 16);
-                        v[1] = f32_to_bf16(h[i][j][2]) | (f32_to_bf16(h[i][j][3]) << 16);
+                        v[0] = f32x2_to_bf16x2(h[i][j][0], h[i][j][1]);
+                        v[1] = f32x2_to_bf16x2(h[i][j][2], h[i][j][3]);
                         *reinterpret_cast<u32x2 *>(hrow + 16 * j) = v;
                     }
                 }
