@@ -1080,17 +1080,39 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         }
         return;
     }
-    if (n_heavy > 0) {
-        gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
-        __syncthreads();  // every wave is done with the first class's ring and table
+    if (n_heavy == 0) {  // one class after another, each balanced over the blocks
+        gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, -1);
+        if constexpr (SMALL > 1) {
+            __syncthreads();
+            if (threadIdx.x >= Tile<32>::THREADS)
+                return;
+            gmm_body<DT, EPI, 32, true>(p, 1, SMALL, -1);
+        }
+        return;
     }
-    const int lpos = n_heavy > 0 ? ((pos - n_heavy) % G + G) % G : -1;
-    gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, lpos);
+    // At least as many heavy tiles as blocks: they go round-robin over the blocks, so the first
+    // heavy_tiles % G blocks run one more of them than the rest.  Those others (the free blocks) start the
+    // light tiles with a run of about one heavy tile's worth each; the rest of the light tiles go
+    // round-robin over all blocks (measured on config 4's GMM2, 364 heavy tiles on 256 blocks: the light
+    // tiles' round-robin then no longer lands on blocks still busy with their second heavy tile).
+    gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
+    __syncthreads();  // every wave is done with the first class's ring and table
+    const int r = heavy_tiles % G;
+    const int nfree = r > 0 ? G - r : 0;
+    const bool is_free = nfree > 0 && pos >= r;
+    const int fpos = pos - r;
+    constexpr int run = DT == DT_BF16 ? 1 : 2;
+    gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, run * nfree + pos, is_free ? fpos * run : 0,
+                                 is_free ? run : 0);
     if constexpr (SMALL > 1) {
         __syncthreads();
         if (threadIdx.x >= Tile<32>::THREADS)
             return;
-        gmm_body<DT, EPI, 32, true>(p, 1, SMALL, lpos);
+        // a plain tile of 32 rows holds 128 W rows, a SwiGLU tile 256: measured 35 and 105 us per heavy
+        // tile against 9 and 45-55 us per light one
+        constexpr int run32 = EPI == EPI_PLAIN ? 4 : CAM_GMM_RUN32;
+        gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * nfree + pos, is_free ? fpos * run32 : 0,
+                                    is_free ? run32 : 0);
     }
 }
 
