@@ -1026,6 +1026,11 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         return;
     }
     constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
+    // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
+    // for bf16) or 32-row tiles (a plain one holds 128 W rows, a SwiGLU one 256: measured 35 and 105 us per
+    // heavy tile against 9 and 45-55 us per light one)
+    constexpr int run = DT == DT_BF16 ? 1 : 2;
+    constexpr int run32 = EPI == EPI_PLAIN ? 4 : CAM_GMM_RUN32;
     int *red = reinterpret_cast<int *>(smem);
     if (threadIdx.x == 0)
         red[0] = 0;
@@ -1046,8 +1051,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     if (heavy_tiles > 0 && heavy_tiles < G && (G & 7) == 0) {
         // Fewer heavy tiles than blocks.  They are split evenly over the 8 XCDs (XCD x takes the run
         // [x hx, (x + 1) hx), consecutive tiles sharing that XCD's L2), so each XCD keeps some blocks free.
-        // The free blocks start on the light tiles at once, `run` in a row each (a 256-row tile costs
-        // about that many weight-streaming 128-row tiles: 2 for 1-byte operands, 1 for bf16); the rest of
+        // The free blocks start on the light tiles at once, `run` (or `run32`) in a row each; the rest of
         // the light tiles go round-robin over all blocks in launch order (every XCD in turn), reaching the
         // heavy blocks as they finish.
         const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, S = G >> 3;
@@ -1059,7 +1063,6 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
                                    (len - slot + S - 1) / S, S);
             __syncthreads();  // every wave is done with the first class's ring and table
         }
-        constexpr int run = DT == DT_BF16 ? 1 : 2;
         int free_before = 0, free_all = 0;
         for (int x = 0; x < 8; ++x) {
             const int fx = max(0, S - heavy_in(x));
@@ -1074,7 +1077,6 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
             __syncthreads();
             if (threadIdx.x >= Tile<32>::THREADS)
                 return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
-            constexpr int run32 = CAM_GMM_RUN32;
             gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * free_all + (int)blockIdx.x,
                                         is_free ? fpos * run32 : 0, is_free ? run32 : 0);
         }
@@ -1101,16 +1103,12 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     const int nfree = r > 0 ? G - r : 0;
     const bool is_free = nfree > 0 && pos >= r;
     const int fpos = pos - r;
-    constexpr int run = DT == DT_BF16 ? 1 : 2;
     gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, run * nfree + pos, is_free ? fpos * run : 0,
                                  is_free ? run : 0);
     if constexpr (SMALL > 1) {
         __syncthreads();
         if (threadIdx.x >= Tile<32>::THREADS)
             return;
-        // a plain tile of 32 rows holds 128 W rows, a SwiGLU tile 256: measured 35 and 105 us per heavy
-        // tile against 9 and 45-55 us per light one
-        constexpr int run32 = EPI == EPI_PLAIN ? 4 : CAM_GMM_RUN32;
         gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * nfree + pos, is_free ? fpos * run32 : 0,
                                     is_free ? run32 : 0);
     }
