@@ -207,8 +207,9 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
 
 // The same DMAs through a buffer resource: the base sits in four SGPRs, the lane's 32-bit byte offset in one
 // VGPR and the k-step's offset in an SGPR, so a DMA needs no 64-bit address registers and no address
-// arithmetic per k-step.  Offsets are 32-bit (every operand here is under 4 GiB); the record count is
-// unbounded.
+// arithmetic per k-step.  Offsets are 32-bit, as the flat addresses' per-lane offsets already are: the C ABI
+// rejects activations or one expert's weights of 4 GiB or more, and the activation scales are a 32nd of the
+// activations.  The record count is unbounded (no range check, as with flat addresses).
 #ifndef CAM_GMM_BUFDMA
 #define CAM_GMM_BUFDMA 1
 #endif
