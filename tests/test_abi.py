@@ -218,3 +218,16 @@ def test_combine_noalloc_rejects_beyond_its_scratch(L):
     assert st == 161001 and "static scratch" in L.camhipGetLastErrorMsg().decode()
     st = L.camhipMoeCombineNormalNoAlloc(P, P, 8, None, P, 4, 2, 1000, 1, 0, 8, P, None, None)
     assert st == 161001 and "hidden" in L.camhipGetLastErrorMsg().decode()
+
+
+@pytest.mark.parametrize("i2", [600064, 262144])
+def test_fused_rejects_operands_past_32bit_offsets(L, i2):
+    # one expert's fp8 weights (2I x H) or h (batch*topk x I) of 4 GiB or more: the grouped GEMMs address
+    # an operand with 32-bit byte offsets
+    st, _, ex, msg = _ws(L, "camhipFusedDeepMoe", P, P, P, P, P, P, P, None, None, None, None, None, None, None,
+                         4096, 7168, 8, i2, 0, 3, 1, 0, 32, 0, 0, P, None, P)
+    assert st != 0 and "4 GiB" in msg, msg
+    st, _, ex, msg = _ws(L, "camhipFusedDeepMoe", P, P, P, P, P, P, P, None, None, None, None, None, None, None,
+                         4096, 7168, 8, 4096, 0, 3, 1, 0, 32, 0, 0, P, None, P)
+    assert st == 0, msg
+    L.camhipReleaseExecutor(ex)

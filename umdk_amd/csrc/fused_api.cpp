@@ -12,6 +12,7 @@
 // decode path, doc/en/cam/CAM API Guide.md:212).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <functional>
@@ -152,6 +153,15 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
     if (!shared)  // the reference's test passes share_smooth_scales with or without a shared expert
         shareSmoothScales = nullptr;
     const bool quantised = weightDtype != CAMHIP_DTYPE_BF16;
+    {
+        // the grouped GEMMs address an operand with 32-bit byte offsets: one expert's weights, the dispatched
+        // rows and h stay under 4 GiB
+        const int64_t esz = weightDtype == CAMHIP_DTYPE_BF16 ? 2 : 1, lim = (int64_t)1 << 32;
+        const int64_t rows = batchSize * topK, i2 = std::max(gmm1HiddenSize, shared ? shareGmm1HiddenSize : 0);
+        F_CHECK(i2 * hidden * esz < lim && rows * hidden * esz < lim && rows * (i2 / 2) * esz < lim,
+                "fused_deep_moe: an expert's weights or the dispatched rows exceed 4 GiB (gmm1 hidden size %lld)",
+                (long long)i2);
+    }
     if (shared) {
         F_CHECK(shareGmm1HiddenSize >= 256 && shareGmm1HiddenSize % 256 == 0,
                 "fused_deep_moe: share gmm1 hidden size %lld must be a multiple of 256",
