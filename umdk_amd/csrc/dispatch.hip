@@ -28,10 +28,12 @@ constexpr int DISP_MAX_K = 16;
 
 // Where the rank of (t,k) within its expert comes from: send_token_idx[t,k] (the layout op's output), or,
 // with send_token_idx == nullptr, chunk_base (the prefill step: chunks of `tpc` tokens, chunk_base[e * nc + c]
-// = entries of expert e in chunks before c) plus the rank inside the chunk, counted here.
+// = entries of expert e in chunks before c) plus chunk_rank[t,k], the rank inside the chunk (the routing
+// kernel's).
 struct RankSrc {
     const int32_t *send_token_idx;
     const int32_t *chunk_base;
+    const int32_t *chunk_rank;
     int tpc;
 };
 
@@ -49,33 +51,11 @@ __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_id
             if (e >= 0 && e < E)
                 dst = send_offset[e] + rs.send_token_idx[(size_t)t * K + lane];
         }
-    } else {
-        // rank inside the chunk (at most 256 entries, row-major (t,k) order): per k, one ballot per 64-entry
-        // window of the chunk's ids marks the entries of the same expert, and those before (t,k) are counted
-        const int c = t / rs.tpc, t0 = c * rs.tpc, nc = (T + rs.tpc - 1) / rs.tpc;
-        const int p0 = t0 * K, pn = min(T, t0 + rs.tpc) * K - p0;
-        int ids[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = u * 64 + lane;
-            const int v = i < pn ? topk_idx[p0 + i] : -1;
-            ids[u] = (v >= 0 && v < E) ? v : -1;
-        }
-        for (int k = 0; k < K; ++k) {
-            const int e = __builtin_amdgcn_readfirstlane(topk_idx[(size_t)t * K + k]);
-            if (e < 0 || e >= E)
-                continue;
-            const int q = (t - t0) * K + k;  // this entry's position in the chunk
-            int cnt = 0;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint64_t m = __ballot(ids[u] == e);
-                const int n = q - u * 64;
-                const uint64_t before = n >= 64 ? ~0ull : n <= 0 ? 0ull : ((1ull << n) - 1);
-                cnt += __popcll(m & before);
-            }
-            if (lane == k)
-                dst = send_offset[e] + rs.chunk_base[(size_t)e * nc + c] + cnt;
+    } else if (lane < K) {
+        const int e = topk_idx[(size_t)t * K + lane];
+        if (e >= 0 && e < E) {
+            const int nc = (T + rs.tpc - 1) / rs.tpc;
+            dst = send_offset[e] + rs.chunk_base[(size_t)e * nc + t / rs.tpc] + rs.chunk_rank[(size_t)t * K + lane];
         }
     }
     if (dst >= cap)  // inconsistent counts: never write outside the output
@@ -296,11 +276,12 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int32_t *send_offset,
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out,
-                           const float *smooth, bool kmajor_scales, const int32_t *chunk_base, int tpc)
+                           const float *smooth, bool kmajor_scales, const int32_t *chunk_base, int tpc,
+                           const int32_t *chunk_rank)
 {
-    if (topk_idx && !send_token_idx && (!chunk_base || tpc < 1 || tpc * K > 256))
+    if (topk_idx && !send_token_idx && (!chunk_base || !chunk_rank || tpc < 1))
         return hipErrorInvalidValue;
-    const RankSrc rs{send_token_idx, chunk_base, tpc};
+    const RankSrc rs{send_token_idx, chunk_base, chunk_rank, tpc};
     if (T == 0)
         return hipSuccess;
     if (H > DISP_NIT * 1024 || K > DISP_MAX_K || (H & 15))

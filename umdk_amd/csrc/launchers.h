@@ -15,11 +15,13 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
                         float *topk_w, hipStream_t s, int64_t *topk_idx64 = nullptr);
 
 // routing that also writes per-chunk histograms of the ids below Ec: chunks of route_tokens_per_block() tokens,
-// chunk_counts[e * nc + c] (the prefill step)
+// chunk_counts[e * nc + c], and each such pick's rank among its chunk's picks of the same expert,
+// chunk_rank[t * K + k] (the prefill step)
 int route_tokens_per_block();
 // (*arrivals is cleared for the launch_scan_notify that follows)
 hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
-                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, hipStream_t s);
+                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, int32_t *chunk_rank,
+                             hipStream_t s);
 
 // ---- dispatch layout (layout.hip)
 struct LayoutPlan {
@@ -57,9 +59,9 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
                            int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false,
-                           const int32_t *chunk_base = nullptr, int tpc = 0);
-// (send_token_idx == nullptr: the rank within the expert is chunk_base[e * nc + t / tpc] plus the rank inside the
-// token's chunk of tpc tokens, counted in the kernel; tpc * K <= 256)
+                           const int32_t *chunk_base = nullptr, int tpc = 0, const int32_t *chunk_rank = nullptr);
+// (send_token_idx == nullptr: the rank within the expert is chunk_base[e * nc + t / tpc] plus chunk_rank[t * K + k],
+// the rank inside the token's chunk of tpc tokens)
 // (fp8: kmajor_scales writes the block scales as [H/128, cap], the layout the grouped GEMMs read)
 // combine without the scatter launch, for callers whose dispatch already wrote inv
 hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,

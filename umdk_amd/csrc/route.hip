@@ -47,7 +47,12 @@ __device__ __forceinline__ uint32_t order_key(float s)
 }
 
 // HIST: the block's 16 tokens are one layout chunk; it also writes the chunk's histogram of the picked
-// ids below Ec (the local experts), chunk_counts[e * gridDim.x + blockIdx.x] for every e < Ec
+// ids below Ec (the local experts), chunk_counts[e * gridDim.x + blockIdx.x] for every e < Ec, and each such
+// pick's rank among the chunk's picks of the same expert in (t,k) order, chunk_rank[t * K + k].  A token's K
+// picks are distinct experts, so that rank is the number of earlier tokens of the chunk that picked the
+// expert: each expert gets a 16-bit mask of the chunk's tokens that picked it (an LDS atomic OR, which no
+// order of the ORs changes), the rank is the popcount of the mask below the token, the count that of the
+// whole mask.
 template <int PER, bool HIST = false>
 __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int T, int E,
@@ -55,7 +60,8 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
                                                                  float *__restrict__ topk_w,
                                                                  int64_t *__restrict__ topk_idx64,
                                                                  int Ec = 0, int32_t *__restrict__ chunk_counts = nullptr,
-                                                                 uint32_t *__restrict__ arrivals = nullptr)
+                                                                 uint32_t *__restrict__ arrivals = nullptr,
+                                                                 int32_t *__restrict__ chunk_rank = nullptr)
 {
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
@@ -128,17 +134,22 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
             topk_idx64[(size_t)t * K + l16] = my_idx;
     }
     if constexpr (HIST) {
+        static_assert(ROUTE_WAVES * 4 <= 32, "a chunk's tokens fit a 32-bit mask");
         if (blockIdx.x == 0 && threadIdx.x == 0)
             *arrivals = 0u;  // the arrival count of the scan launch that follows on the stream
-        __shared__ int32_t hist[ROUTE_MAX_PER_LANE * 16];
+        __shared__ uint32_t picked[ROUTE_MAX_PER_LANE * 16];  // per expert: the chunk's tokens that picked it
         for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
-            hist[e] = 0;
+            picked[e] = 0u;
         __syncthreads();
-        if (l16 < K && live && my_idx < Ec)
-            atomicAdd(&hist[my_idx], 1);  // counts only: the order of the adds does not matter
+        const int tl = t - blockIdx.x * ROUTE_WAVES * 4;  // the token's place in the chunk
+        const bool local = l16 < K && live && my_idx < Ec;
+        if (local)
+            atomicOr(&picked[my_idx], 1u << tl);
         __syncthreads();
+        if (local)
+            chunk_rank[(size_t)t * K + l16] = __popc(picked[my_idx] & ((1u << tl) - 1u));
         for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
-            chunk_counts[(size_t)e * gridDim.x + blockIdx.x] = hist[e];
+            chunk_counts[(size_t)e * gridDim.x + blockIdx.x] = __popc(picked[e]);
     }
 }
 
@@ -171,18 +182,19 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
 int route_tokens_per_block() { return ROUTE_WAVES * 4; }
 
 hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
-                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, hipStream_t s)
+                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, int32_t *chunk_rank,
+                             hipStream_t s)
 {
     if (T == 0)
         return hipSuccess;
-    if (E > 16 * ROUTE_MAX_PER_LANE || K > 16 || Ec > E || Ec < 1)
+    if (E > 16 * ROUTE_MAX_PER_LANE || K > 16 || Ec > E || Ec < 1 || !chunk_rank)
         return hipErrorInvalidValue;
     const int grid = (T + ROUTE_WAVES * 4 - 1) / (ROUTE_WAVES * 4);
     const dim3 g(grid), b(ROUTE_WAVES * 64);
     const int per = (E + 15) >> 4;
 #define ROUTE_HIST_CASE(P)                                                                                          \
     hipLaunchKernelGGL((route_kernel<P, true>), g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, nullptr, Ec,   \
-                       chunk_counts, arrivals)
+                       chunk_counts, arrivals, chunk_rank)
     if (per <= 1)
         ROUTE_HIST_CASE(1);
     else if (per <= 2)
