@@ -99,6 +99,54 @@ def test_int8_gmm2_bit_exact_vs_oracle(ops, counts, H, I):
     assert np.array_equal(b16(y), ref)
 
 
+@pytest.mark.parametrize("counts", [[700, 5, 1100, 30, 400], [1300, 40, 900, 150, 3]])
+def test_int8_256_row_tiles_vs_oracle(ops, counts):
+    # experts of >= 384 rows take 256-row tiles once the reduction has >= 16 k-steps: GMM1 at H = 2048 (SwiGLU
+    # with the fp32 h and row maxima), GMM2 at I = 2048 (plain, bit-exact); the others take 128-row tiles in the
+    # same launch
+    print(f"int8 256-row tiles counts={counts}", flush=True)
+    g = gen(sum(counts))
+    L, M = len(counts), sum(counts)
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    H, I = 2048, 256
+    x = torch.randint(-127, 128, (M, H), generator=g).to(torch.int8)
+    xs = torch.rand(M, generator=g) * 0.04
+    w1 = w_int8(g, (L, 2 * I, H))
+    s1 = ch_scale(g, (L, 2 * I))
+    hq, hs = ops.grouped_matmul_swiglu(x.cuda(), xs.cuda(), cnt.cuda(), w1.cuda(), s1.cuda(), 2)
+    q_ref, s_ref = orc.quant_rows_int8(orc.gmm1_swiglu_int8(x.numpy(), xs.numpy(), cnt.numpy(), w1.numpy(),
+                                                            s1.numpy()))
+    check_requant(hq, hs, q_ref, s_ref)
+    H, I = 512, 2048
+    hq = torch.randint(-127, 128, (M, I), generator=g).to(torch.int8)
+    hs = torch.rand(M, generator=g) * 0.01
+    w2 = w_int8(g, (L, H, I))
+    s2 = ch_scale(g, (L, H))
+    y = ops.grouped_matmul(hq.cuda(), hs.cuda(), cnt.cuda(), w2.cuda(), s2.cuda())
+    assert np.array_equal(b16(y), orc.gmm2_int8(hq.numpy(), hs.numpy(), cnt.numpy(), w2.numpy(), s2.numpy()))
+
+
+def test_int8_gmm2_more_heavy_tiles_than_blocks(ops):
+    # 18 heavy M-tiles x 16 N-tiles = 288 256-row tiles on 256 blocks: the blocks with one heavy tile fewer
+    # start the 128-row tiles with runs of their own.  Reference on the GPU: int8 x int8 sums in fp64 are exact
+    # (|sum| < 2^53), then the kernel's fp32 sequence ((float)acc * w_scale) * x_scale and bf16 rounding
+    counts, H, I = [2100, 40, 2100, 150, 3], 4096, 2048
+    print(f"int8 gmm2 counts={counts} H={H} I={I}", flush=True)
+    g = gen(5)
+    L, M = len(counts), sum(counts)
+    hq = torch.randint(-127, 128, (M, I), generator=g).to(torch.int8).cuda()
+    hs = (torch.rand(M, generator=g) * 0.01).cuda()
+    w2 = w_int8(g, (L, H, I)).cuda()
+    s2 = ch_scale(g, (L, H)).cuda()
+    y = ops.grouped_matmul(hq, hs, torch.tensor(counts, dtype=torch.int64).cuda(), w2, s2)
+    off = 0
+    for e, c in enumerate(counts):
+        acc = (hq[off:off + c].double() @ w2[e].double().T).float()
+        ref = ((acc * s2[e][None, :]) * hs[off:off + c, None]).bfloat16()
+        assert torch.equal(y[off:off + c].view(torch.int16), ref.view(torch.int16)), f"expert {e}"
+        off += c
+
+
 def test_int8_gemm_large_vs_torch(ops):
     # prefill-sized rows per expert (the 8-wave kernel, 256-row tile): exact int64 sums on the CPU
     counts, H, I = [700, 0, 1100, 520], 1024, 256
