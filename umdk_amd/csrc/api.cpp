@@ -438,7 +438,7 @@ camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(const float *logits, const
             if (e != hipSuccess)
                 return e;
             return cam::launch_dispatch(x, topkIdx, send_off, nullptr, T, H, K, L, 0, cap, q, recvX, recvXScales,
-                                        expandIdx, s, combineRowMap, nullptr, kmajor, counts, tpc, chunk_rank);
+                                        expandIdx, s, combineRowMap, nullptr, kmajor, counts, tpc, chunk_rank, L < E);
         },
         workspaceSize, executor);
 }

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
     RankSrc rs, int T, int H, int K, int E, int rank, int cap, int nchunk,
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
-    int32_t *__restrict__ inv_out, int kmajor)
+    int32_t *__restrict__ inv_out, int kmajor, int skip_unrouted)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
@@ -77,6 +77,17 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     if (item >= (long)T * nchunk)
         return;
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
+    // skip_unrouted (a rank holding some of the experts): a token none of whose picks is an expert of this rank
+    // reads nothing, only its row-map entries are written (config 4, 32 of 256 experts local: 40% of the
+    // tokens, the layer 2-3 us faster; with every expert local the check measured 0.7 us slower per step)
+    if (skip_unrouted && topk_idx) {
+        const int e0 = lane < K ? topk_idx[(size_t)t * K + lane] : -1;
+        if (__ballot(e0 >= 0 && e0 < E) == 0) {
+            if (inv_out && j == 0 && lane < K)
+                inv_out[(size_t)t * K + lane] = -1;
+            return;
+        }
+    }
     // the slice of x is requested first, so its loads are in flight while the destination rows resolve
     if constexpr (MODE == QUANT_NONE) {
         // lane l copies columns [1024 j + 8 l, +8) and [1024 j + 512 + 8 l, +8): each 16-byte
@@ -277,7 +288,7 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s, int32_t *inv_out,
                            const float *smooth, bool kmajor_scales, const int32_t *chunk_base, int tpc,
-                           const int32_t *chunk_rank)
+                           const int32_t *chunk_rank, bool skip_unrouted)
 {
     if (topk_idx && !send_token_idx && (!chunk_base || !chunk_rank || tpc < 1))
         return hipErrorInvalidValue;
@@ -293,7 +304,7 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
     switch (quant_mode) {
     case QUANT_NONE:
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_NONE>, grid_chunk, block, 0, s, x, topk_idx, send_offset,
-                           rs, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out, 0);
+                           rs, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out, 0, skip_unrouted ? 1 : 0);
         break;
     case QUANT_INT8_TOKEN:
         hipLaunchKernelGGL(dispatch_int8_kernel<false>, dim3((T + DISP_WAVES - 1) / DISP_WAVES), block, 0, s, x,
@@ -310,7 +321,7 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(dispatch_chunk_kernel<QUANT_FP8_BLOCK>, grid_chunk, block, 0, s, x, topk_idx,
                            send_offset, rs, T, H, K, E, rank, cap, nchunk, ex, scales, expand_idx, inv_out,
-                           kmajor_scales ? 1 : 0);
+                           kmajor_scales ? 1 : 0, skip_unrouted ? 1 : 0);
         break;
     default:
         return hipErrorInvalidValue;

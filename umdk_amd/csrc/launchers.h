@@ -59,9 +59,11 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
                            const int32_t *send_token_idx, int T, int H, int K, int E, int rank, int cap, int quant_mode,
                            void *expand_x, float *scales, int32_t *expand_idx, hipStream_t s,
                            int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false,
-                           const int32_t *chunk_base = nullptr, int tpc = 0, const int32_t *chunk_rank = nullptr);
+                           const int32_t *chunk_base = nullptr, int tpc = 0, const int32_t *chunk_rank = nullptr,
+                           bool skip_unrouted = false);
 // (send_token_idx == nullptr: the rank within the expert is chunk_base[e * nc + t / tpc] plus chunk_rank[t * K + k],
-// the rank inside the token's chunk of tpc tokens)
+// the rank inside the token's chunk of tpc tokens; skip_unrouted: tokens with no pick in [0, E) read nothing, for a
+// rank that holds only some of the experts)
 // (fp8: kmajor_scales writes the block scales as [H/128, cap], the layout the grouped GEMMs read)
 // combine without the scatter launch, for callers whose dispatch already wrote inv
 hipError_t launch_combine_gather(const uint16_t *y, const int32_t *expand_idx, int N, const int32_t *recv_count_last,
