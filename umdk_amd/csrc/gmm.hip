@@ -16,19 +16,19 @@
 //     (block_epilogue_per_token_dequant.hpp:338-361).
 //
 // Kernel design (gfx950):
-//   * 128 x 256 output tiles (SwiGLU: 128 rows x 128 h-columns = 128 gate +
-//     128 up rows of W), 4 waves in a 2 x 2 grid, 64 x 128 per wave as 4 x 8
-//     MFMA 16x16 tiles: v_mfma_f32_16x16x32_bf16, or
-//     v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales for fp8.
-//   * Operands stream through a 3-stage LDS ring by direct global->LDS DMA
-//     (global_load_lds_dwordx4): no staging registers, and two k-steps of
-//     loads stay in flight while one is multiplied.  Each k-step is 128 bytes
-//     of every A and W row (64 bf16 / 128 fp8 elements); the fp8 activation
-//     scales of the k-step ride the same DMA (4-byte lanes, read k-major
-//     [K/128, M] so that one k-step's scales of 64 rows are one contiguous
-//     256-byte run; row-major scales are transposed first).  A wave's loads
-//     are counted with s_waitcnt vmcnt and published with a bare s_barrier
-//     (no fence, so outstanding prefetches are not drained).
+//   * Output tiles of 256, 128 or 32 rows x 256 W rows (SwiGLU: the gate and up rows of one 128-column
+//     block of h; the decode plain GEMM 128 W rows), picked per expert from its row count (the Tile
+//     struct below); the 128/256-row tiles run 8 waves in a 2 x 4 grid, the 32-row tile 4 waves.  MFMA
+//     16x16: v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8, or v_mfma_scale_f32_16x16x128_f8f6f4 with
+//     unit scales for fp8.
+//   * Operands stream through a ring of LDS stages by direct global->LDS DMA (global_load_lds_dwordx4, or
+//     buffer_load_dwordx4 ... lds through a buffer resource for the 128/256-row tiles): no staging
+//     registers, and further k-steps stay in flight while one is multiplied.  Each k-step is 128 bytes of
+//     every A and W row (64 bf16 / 128 one-byte elements); the fp8 activation scales of the k-step ride the
+//     same DMA (4-byte lanes, read k-major [K/128, M] so that one k-step's scales of 64 rows are one
+//     contiguous 256-byte run; row-major scales are transposed first).  A wave's loads are counted with
+//     s_waitcnt vmcnt and published with a bare s_barrier (no fence, so outstanding prefetches are not
+//     drained).
 //   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row >> 1) & 7:
 //     each lane fetches the global chunk that belongs at its DMA slot, so
 //     fragment reads spread over all banks.
@@ -36,7 +36,8 @@
 //     accumulators are four consecutive output columns of one row: the
 //     epilogue stores 8 contiguous bytes per lane without a transpose.
 //   * fp8: one MFMA of K=128 per (i,j) per k-step covers exactly one scale
-//     block, so acc += mfma(...) * (a_scale[m] * w_scale[n-block]).
+//     block, so acc += mfma(...) * (a_scale[m] * w_scale[n-block]), applied by the VALU one fragment row
+//     after the MFMA that produced it.
 //   * Persistent grid (one block per CU) walking tiles expert by expert in
 //     groups of 8 M-tiles x all N-tiles (M fastest), remapped so that the
 //     blocks of one XCD take consecutive tiles: they share A and W tiles in
