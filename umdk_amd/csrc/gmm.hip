@@ -100,67 +100,108 @@ template <int BM_, int BN_ = GBN> struct Tile {
 #endif
 constexpr int small_bn(int bm, int epi) { return bm == 32 && epi == 0 ? CAM_GMM_SMALL_PLAIN_BN : GBN; }
 
-struct GroupTable {
-    int tile_prefix[G_MAX_L + 1];  // exclusive prefix of M-tiles per expert
-    int row_off[G_MAX_L + 1];      // exclusive prefix of rows per expert
+// Expert tables of a launch, built once at kernel start: per tile class (256-, 128- and 32-row tiles) the
+// inclusive prefix of M-tiles per expert, and the inclusive prefix of rows per expert (the exclusive prefix
+// of expert e is entry e-1, or 0 for e = 0; no entry for it keeps the tables within the LDS budget).
+constexpr int G_NCLASS = 3;
+constexpr int tile_class(int bm) { return bm >= 256 ? 0 : bm >= 128 ? 1 : 2; }
+struct GroupTables {
+    int tile_end[G_NCLASS][G_MAX_L];
+    int row_end[G_MAX_L];
+};
+// the experts each class takes: a row count in [lo, hi) (lo >= hi: the class is not used)
+struct ClassRanges {
+    int lo[G_NCLASS], hi[G_NCLASS];
 };
 
-// Block-wide exclusive scans of the M-tiles and rows per expert.  Only experts with a row count in
-// [lo, hi) get tiles (a launch may split the experts between two tile heights); the row offsets
-// count every expert (they locate segments in dispatch order).
-template <int GBM, int GTHREADS>
-__device__ void build_group_table(const int64_t *__restrict__ group_list, int L, GroupTable &gt, int *scratch, int lo,
-                                  int hi)
+// Diagnostic build only (-DCAM_GMM_TIMELINE): every block records, per tile, its wall-clock start and end
+// (100 MHz constant clock) with the tile's class, expert and index, into 128 slots per block;
+// camhipDebugGmmTimeline copies them out.  Off in every product build.
+#ifdef CAM_GMM_TIMELINE
+constexpr int G_TL_SLOTS = 128, G_TL_BLOCKS = 1024;
+__device__ uint64_t g_cam_tl[G_TL_BLOCKS * G_TL_SLOTS][3];
+#define CAM_TL_DECL int tl_k = BM >= 256 ? 0 : BM >= 128 ? 32 : 64; uint64_t tl_t0 = wall_clock64();
+#define CAM_TL_REC(e, tile)                                                                                     \
+    do {                                                                                                        \
+        const uint64_t tl_t1 = wall_clock64();                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < G_TL_BLOCKS && tl_k < G_TL_SLOTS) {                                \
+            uint64_t *r = g_cam_tl[blockIdx.x * G_TL_SLOTS + tl_k];                                              \
+            r[0] = ((uint64_t)blockIdx.x << 48) | ((uint64_t)BM << 36) | ((uint64_t)EPI << 32) |                 \
+                   ((uint64_t)(e) << 20) | (uint64_t)(tile);                                                    \
+            r[1] = tl_t0;                                                                                       \
+            r[2] = tl_t1;                                                                                       \
+        }                                                                                                       \
+        ++tl_k;                                                                                                 \
+        tl_t0 = tl_t1;                                                                                          \
+    } while (0)
+#else
+#define CAM_TL_DECL
+#define CAM_TL_REC(e, tile)
+#endif
+
+// Block-wide exclusive scans of the M-tiles of each tile class and of the rows per expert, from one read of
+// the counts.  Only experts with a row count in a class's [lo, hi) get tiles of that class (a launch may
+// split the experts between tile heights); the row offsets count every expert (they locate segments in
+// dispatch order).
+template <int GTHREADS>
+__device__ void build_group_tables(const int64_t *__restrict__ group_list, int L, GroupTables &gt, int *scratch,
+                                   const ClassRanges &cr)
 {
+    constexpr int NQ = G_NCLASS + 1;  // tile counts per class, then rows
+    constexpr int BMS[G_NCLASS] = {256, 128, 32};
     const int tid = threadIdx.x;
     const int per = (L + GTHREADS - 1) / GTHREADS;
-    int tsum = 0, rsum = 0;
+    int cnt[4] = {0, 0, 0, 0};
+    auto add = [&](int c, int *v) {
+#pragma unroll
+        for (int k = 0; k < G_NCLASS; ++k)
+            v[k] += (c >= cr.lo[k] && c < cr.hi[k]) ? (c + BMS[k] - 1) / BMS[k] : 0;
+        v[G_NCLASS] += c;
+    };
     for (int q = 0; q < per; ++q) {
         const int e = tid * per + q;
-        if (e < L) {
-            const int c = (int)group_list[e];
-            tsum += (c >= lo && c < hi) ? (c + GBM - 1) / GBM : 0;
-            rsum += c;
-        }
+        if (e < L)
+            add((int)group_list[e], cnt);
     }
     // exclusive scan: within each wave by lane shuffles, then over the waves' totals
     constexpr int NWV = GTHREADS / 64;
     const int lane = tid & 63, wv = tid >> 6;
-    int ti = tsum, ri = rsum;
+    int inc[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k)
+        inc[k] = cnt[k];
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const int tu = __shfl_up(ti, d, 64), ru = __shfl_up(ri, d, 64);
-        if (lane >= d) {
-            ti += tu;
-            ri += ru;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int u = __shfl_up(inc[k], d, 64);
+            if (lane >= d)
+                inc[k] += u;
         }
     }
     if (lane == 63) {
-        scratch[wv] = ti;
-        scratch[NWV + wv] = ri;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k)
+            scratch[k * NWV + wv] = inc[k];
     }
     __syncthreads();
-    int ta = ti - tsum, ra = ri - rsum, at = 0, ar = 0;
+    int run[NQ];
 #pragma unroll
-    for (int v = 0; v < NWV; ++v) {
-        const int x = scratch[v], y = scratch[NWV + v];
-        ta += v < wv ? x : 0;
-        ra += v < wv ? y : 0;
-        at += x;
-        ar += y;
-    }
-    if (tid == 0) {
-        gt.tile_prefix[L] = at;
-        gt.row_off[L] = ar;
+    for (int k = 0; k < NQ; ++k) {
+        int ex = inc[k] - cnt[k];
+#pragma unroll
+        for (int v = 0; v < NWV; ++v)
+            ex += v < wv ? scratch[k * NWV + v] : 0;
+        run[k] = ex;
     }
     for (int q = 0; q < per; ++q) {
         const int e = tid * per + q;
         if (e < L) {
-            const int c = (int)group_list[e];
-            gt.tile_prefix[e] = ta;
-            gt.row_off[e] = ra;
-            ta += (c >= lo && c < hi) ? (c + GBM - 1) / GBM : 0;
-            ra += c;
+            add((int)group_list[e], run);
+#pragma unroll
+            for (int k = 0; k < G_NCLASS; ++k)
+                gt.tile_end[k][e] = run[k];
+            gt.row_end[e] = run[G_NCLASS];
         }
     }
     __syncthreads();
@@ -249,20 +290,21 @@ __device__ __forceinline__ void lds_sync()
 // (first < 0: balanced placement, see below), preceded by a run of rn tiles rs, rs + rstride, ... (an
 // increasing sequence: the first index past the class's tiles ends it).
 template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM)>
-__device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int first, int rs = 0, int rn = 0,
+__device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gtab, int first, int rs = 0, int rn = 0,
                                          int rstride = 1)
 {
     using TC = Tile<BM, small_bn(BM, EPI)>;
     constexpr int TBN = TC::BN;
-    constexpr int GTHREADS = TC::THREADS, NW = TC::NWAVES;
+    constexpr int NW = TC::NWAVES;
     constexpr int GBM = TC::BM, WM = TC::WM, WN = TC::WN, IF = TC::IF, JF = TC::JF;
     constexpr int GSTAGES = TC::STAGES, STAGE_BYTES = TC::STAGE_BYTES;
     constexpr int A_BYTES = TC::A_BYTES, B_BYTES = TC::B_BYTES, A_LOADS = TC::A_LOADS, B_LOADS = TC::B_LOADS;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-    GroupTable *gt = reinterpret_cast<GroupTable *>(smem + GSTAGES * STAGE_BYTES);
-    int *scratch = reinterpret_cast<int *>(gt + 1);  // 2*GMAX_THREADS ints: table scan, then the fp8 amax exchange
-
-    build_group_table<GBM, GTHREADS>(p.group_list, p.L, *gt, scratch, lo, hi);
+    // the epilogue's exchange area (fp8 amax, int8 row maxima) follows this class's ring
+    int *scratch = reinterpret_cast<int *>(smem + GSTAGES * STAGE_BYTES);
+    const int *tile_end = gtab->tile_end[tile_class(BM)];
+    auto tile_prefix = [&](int e) { return e > 0 ? tile_end[e - 1] : 0; };
+    auto row_off = [&](int e) { return e > 0 ? gtab->row_end[e - 1] : 0; };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -277,7 +319,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
     const int nk = (int)(kbytes / GKB);
     const int half_n = p.N / 2;                    // I for SwiGLU
     const int ntn = SWIGLU ? half_n / 128 : p.N / TBN;
-    const int total = __builtin_amdgcn_readfirstlane(gt->tile_prefix[p.L]) * ntn;
+    const int total = __builtin_amdgcn_readfirstlane(tile_prefix(p.L)) * ntn;
 
     // first < 0: this launch has one tile class, so balance it: with R = ceil(total / grid) rounds, only
     // the first ceil(total / R) blocks (rounded up to whole XCDs) take tiles, R each at most.  A weight
@@ -313,15 +355,15 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         int lo = 0, hi = p.L - 1;
         while (lo < hi) {  // last e with tile_prefix[e]*ntn <= tile
             const int mid = (lo + hi + 1) >> 1;
-            if (gt->tile_prefix[mid] * ntn <= tile)
+            if (tile_end[mid - 1] * ntn <= tile)
                 lo = mid;
             else
                 hi = mid - 1;
         }
         const int e = __builtin_amdgcn_readfirstlane(lo);
         c.e = e;
-        const int mt_e = __builtin_amdgcn_readfirstlane(gt->tile_prefix[e + 1] - gt->tile_prefix[e]);
-        const int local = __builtin_amdgcn_readfirstlane(tile - gt->tile_prefix[e] * ntn);
+        const int mt_e = __builtin_amdgcn_readfirstlane(tile_end[e] - tile_prefix(e));
+        const int local = __builtin_amdgcn_readfirstlane(tile - tile_prefix(e) * ntn);
         // within the expert: groups of up to 8 M-tiles, N-tiles in turn, the group's M-tiles
         // fastest -- a run of consecutive tiles (one XCD's share of a round) covers ~8 A row blocks
         // x a few W column blocks, so both operands are re-read from that XCD's L2
@@ -329,8 +371,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         const int grp = local / (GM * ntn), rem = local % (GM * ntn);
         const int gm = min(GM, mt_e - grp * GM);
         const int nt = rem / gm, mt = grp * GM + rem % gm;
-        const int seg0 = __builtin_amdgcn_readfirstlane(gt->row_off[e]);
-        c.seg1 = min(__builtin_amdgcn_readfirstlane(gt->row_off[e + 1]), p.M);  // never write past row M
+        const int seg0 = __builtin_amdgcn_readfirstlane(row_off(e));
+        c.seg1 = min(__builtin_amdgcn_readfirstlane(gtab->row_end[e]), p.M);  // never write past row M
         c.row0 = seg0 + mt * GBM;
         c.n0 = SWIGLU ? nt * 128 : nt * TBN;  // first h-column (SwiGLU) or W row (plain)
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
@@ -601,6 +643,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
         };
         int kt = 0, tile = seq(0);
         Ctx c;
+        CAM_TL_DECL
         if (tile < total) {
             setup(tile, c);
             prime(c);
@@ -729,6 +772,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
             bar();
             dequant_int8(c);
             epilogue(c);
+            CAM_TL_REC(c.e, tile);
             // int8: the dequantisation's loads have landed before the next tile (otherwise the compiler,
             // unsure of them, waits for every DMA in flight inside the k-loop)
             if constexpr (INT8)
@@ -754,6 +798,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
             return;
         Ctx cur, nxt;
         setup(tile, cur);
+        CAM_TL_DECL
         int kb = 0;          // the block's k-steps before the current tile
         bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
         while (true) {
@@ -894,9 +939,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                         mm(w0, ks + 1, act);
                     }
                 };
-                if (cur.active)
+                if (TC::WAVES_M == 1 || cur.active)  // (one row-wave: a tile always has rows for it)
                     kloop(std::true_type{});
-                else
+                else if constexpr (TC::WAVES_M > 1)
                     kloop(std::false_type{});
 #pragma unroll
                 for (int j = 0; j < JF; ++j)  // the last row's pending results
@@ -952,9 +997,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                         mm(r1, ks + GSTAGES, act);
                     }
                 };
-                if (cur.active)
+                if (TC::WAVES_M == 1 || cur.active)  // (one row-wave: a tile always has rows for it)
                     kloop(std::true_type{});
-                else
+                else if constexpr (TC::WAVES_M > 1)
                     kloop(std::false_type{});
             }
 
@@ -964,6 +1009,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, int lo, int hi, int f
                 bar();
             }
             epilogue(cur);
+            CAM_TL_REC(cur.e, tile);
             kb += nk;
             if (!has_next)
                 break;
@@ -983,10 +1029,31 @@ __device__ __forceinline__ int xcd_position()
     return (G & 7) ? (int)blockIdx.x : (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
 }
 
+// LDS of a launch: a class's ring of stages, then that class's epilogue exchange area; the expert tables
+// sit at the end of the launch's LDS (the same place for every class of a launch).
+template <int BM, int BN = GBN> constexpr size_t ring_bytes() { return Tile<BM, BN>::STAGES * Tile<BM, BN>::STAGE_BYTES; }
+template <int BM, int BN = GBN> constexpr size_t exchange_bytes()
+{
+    return (size_t)Tile<BM, BN>::WAVES_N * BM * sizeof(float);  // [WAVES_N][BM] row maxima
+}
+template <int BM, int BN = GBN> constexpr size_t class_bytes() { return ring_bytes<BM, BN>() + exchange_bytes<BM, BN>(); }
+constexpr size_t cmax(size_t a, size_t b) { return a > b ? a : b; }
+constexpr size_t G_LDS_SMALL_BYTES = cmax(class_bytes<32, GBN>(), class_bytes<32, 128>()) + sizeof(GroupTables);
+constexpr size_t G_LDS_BIG_BYTES =
+    cmax(cmax(class_bytes<256>(), class_bytes<128>()), cmax(class_bytes<32, GBN>(), class_bytes<32, 128>())) +
+    sizeof(GroupTables);
+static_assert(G_LDS_SMALL_BYTES <= 163840 && G_LDS_BIG_BYTES <= 163840, "LDS budget of a gfx950 workgroup");
+// the table scan's per-wave totals (before any ring use)
+static_assert(sizeof(int) * 4 * (GMAX_THREADS / 64) <= ring_bytes<32, 128>(), "table-scan scratch");
+
 // Decode-sized segments: the 32-row tile (4 waves).
 template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_small(GmmArgs p)
 {
-    gmm_body<DT, EPI, 32>(p, 0, 0x7fffffff, -1);
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_SMALL_BYTES - sizeof(GroupTables));
+    build_group_tables<Tile<32>::THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem),
+                                          ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
+    gmm_body<DT, EPI, 32>(p, gt, -1);
 }
 
 // Prefill: 8 waves, 128- or 256-row tile picked per launch from the actual rows per touched
@@ -1006,6 +1073,9 @@ constexpr int G_SMALL_ROWS = CAM_GMM_SMALL_ROWS;
 #define CAM_GMM_RUN32 3
 #endif
 
+// Between two tile classes the block meets at an LDS-only barrier (lds_sync): both prefill loops have drained
+// their DMAs before the last epilogue, so only the ring's LDS reads must be complete; __syncthreads would also
+// wait for the epilogue's global stores (measured 2-6 us per class switch on config 4's GEMMs).
 // Prefill: 8 waves.  With the 256-row tile allowed, the experts holding at least G_HEAVY_ROWS rows run
 // 256-row tiles first, then the rest 128-row tiles -- one launch, the longest tiles first, the tile
 // sequence of each block continuing round-robin from the first class into the second, and (fp8, bf16) from
@@ -1015,38 +1085,30 @@ constexpr int G_SMALL_ROWS = CAM_GMM_SMALL_ROWS;
 // (at most three M-tiles each) weights are fetched nontemporally.
 template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
 {
-    // the first bytes of the dynamic LDS serve as the reduction slot before the tile body starts
-    // (a static __shared__ array would push the 1 KiB-aligned dynamic region past the LDS limit)
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
     const int pos = xcd_position();
     // short reductions keep the 128-row tile: the 256-row tile's per-tile ring fill and drain would
     // not amortise over fewer than 16 k-steps (at 16, GMM2 of DeepSeek-V3's shapes: the M = 65536 fp8 GMM2
     // 1.71 vs 1.57 PFLOPS, int8 1.97 vs 1.67 POPS, config 4's fp8 GMM2 116 vs 122 us)
     const int nk = (int)((uint32_t)p.K * (DT == DT_BF16 ? 2 : 1) / GKB);
-    if (!p.allow256 || nk < CAM_GMM_MIN_NK256) {
-        gmm_body<DT, EPI, 128>(p, 0, 0x7fffffff, -1);
+    constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
+    const bool tall = p.allow256 && nk >= CAM_GMM_MIN_NK256;
+    // every class's expert table, from one read of the counts
+    build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem),
+                                     tall ? ClassRanges{{G_HEAVY_ROWS, SMALL, 1}, {0x7fffffff, G_HEAVY_ROWS, SMALL}}
+                                          : ClassRanges{{0, 0, 0}, {0, 0x7fffffff, 0}});
+    if (!tall) {
+        gmm_body<DT, EPI, 128>(p, gt, -1);
         return;
     }
-    constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
     // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
     // for bf16) or 32-row tiles (a plain one holds 128 W rows, a SwiGLU one 256: measured 35 and 105 us per
     // heavy tile against 9 and 45-55 us per light one)
     constexpr int run = DT == DT_BF16 ? 1 : 2;
     constexpr int run32 = EPI == EPI_PLAIN ? 4 : CAM_GMM_RUN32;
-    int *red = reinterpret_cast<int *>(smem);
-    if (threadIdx.x == 0)
-        red[0] = 0;
-    __syncthreads();
-    int heavy = 0;  // 256-row tiles of the heavy experts
-    for (int e = threadIdx.x; e < p.L; e += blockDim.x) {
-        const int c = (int)p.group_list[e];
-        heavy += c >= G_HEAVY_ROWS ? (c + 255) / 256 : 0;
-    }
-    if (heavy)
-        atomicAdd(&red[0], heavy);
-    __syncthreads();
-    const int n_heavy = red[0];
-    __syncthreads();
+    const int n_heavy = gt->tile_end[0][p.L - 1];  // 256-row M-tiles of the heavy experts
+    const bool has_mid = gt->tile_end[1][p.L - 1] > 0, has_small = gt->tile_end[2][p.L - 1] > 0;
     const int G = gridDim.x;
     // 256-row tiles: heavy M-tiles x N-tiles
     const int heavy_tiles = n_heavy * (EPI != EPI_PLAIN ? p.N / 2 / 128 : p.N / 256);
@@ -1061,9 +1123,9 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
         const int len = heavy_in(xcd);
         if (slot < len) {
-            gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, 0x3fffffff, xcd * hx + slot,
+            gmm_body<DT, EPI, 256>(p, gt, 0x3fffffff, xcd * hx + slot,
                                    (len - slot + S - 1) / S, S);
-            __syncthreads();  // every wave is done with the first class's ring and table
+            lds_sync();  // every wave is done with the first class's ring
         }
         int free_before = 0, free_all = 0;
         for (int x = 0; x < 8; ++x) {
@@ -1073,24 +1135,30 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         }
         const bool is_free = slot >= len;
         const int fpos = free_before + slot - len;  // the block's rank among the free blocks
-        gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, run * free_all + (int)blockIdx.x,
-                                     is_free ? fpos * run : 0, is_free ? run : 0);
+        if (has_mid)
+            gmm_body<DT, EPI, 128, true>(p, gt, run * free_all + (int)blockIdx.x,
+                                         is_free ? fpos * run : 0, is_free ? run : 0);
         if constexpr (SMALL > 1) {
-            __syncthreads();
-            if (threadIdx.x >= Tile<32>::THREADS)
-                return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
-            gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * free_all + (int)blockIdx.x,
-                                        is_free ? fpos * run32 : 0, is_free ? run32 : 0);
+            if (has_small) {
+                lds_sync();
+                if (threadIdx.x >= Tile<32>::THREADS)
+                    return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
+                gmm_body<DT, EPI, 32, true>(p, gt, run32 * free_all + (int)blockIdx.x,
+                                            is_free ? fpos * run32 : 0, is_free ? run32 : 0);
+            }
         }
         return;
     }
     if (n_heavy == 0) {  // one class after another, each balanced over the blocks
-        gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, -1);
+        if (has_mid)
+            gmm_body<DT, EPI, 128, true>(p, gt, -1);
         if constexpr (SMALL > 1) {
-            __syncthreads();
-            if (threadIdx.x >= Tile<32>::THREADS)
-                return;
-            gmm_body<DT, EPI, 32, true>(p, 1, SMALL, -1);
+            if (has_small) {
+                lds_sync();
+                if (threadIdx.x >= Tile<32>::THREADS)
+                    return;
+                gmm_body<DT, EPI, 32, true>(p, gt, -1);
+            }
         }
         return;
     }
@@ -1099,31 +1167,25 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     // light tiles with a run of about one heavy tile's worth each; the rest of the light tiles go
     // round-robin over all blocks (measured on config 4's GMM2, 364 heavy tiles on 256 blocks: the light
     // tiles' round-robin then no longer lands on blocks still busy with their second heavy tile).
-    gmm_body<DT, EPI, 256>(p, G_HEAVY_ROWS, 0x7fffffff, pos);
-    __syncthreads();  // every wave is done with the first class's ring and table
+    gmm_body<DT, EPI, 256>(p, gt, pos);
+    lds_sync();  // every wave is done with the first class's ring
     const int r = heavy_tiles % G;
     const int nfree = r > 0 ? G - r : 0;
     const bool is_free = nfree > 0 && pos >= r;
     const int fpos = pos - r;
-    gmm_body<DT, EPI, 128, true>(p, SMALL, G_HEAVY_ROWS, run * nfree + pos, is_free ? fpos * run : 0,
-                                 is_free ? run : 0);
+    if (has_mid)
+        gmm_body<DT, EPI, 128, true>(p, gt, run * nfree + pos, is_free ? fpos * run : 0,
+                                     is_free ? run : 0);
     if constexpr (SMALL > 1) {
-        __syncthreads();
-        if (threadIdx.x >= Tile<32>::THREADS)
-            return;
-        gmm_body<DT, EPI, 32, true>(p, 1, SMALL, run32 * nfree + pos, is_free ? fpos * run32 : 0,
-                                    is_free ? run32 : 0);
+        if (has_small) {
+            lds_sync();
+            if (threadIdx.x >= Tile<32>::THREADS)
+                return;
+            gmm_body<DT, EPI, 32, true>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0,
+                                        is_free ? run32 : 0);
+        }
     }
 }
-
-template <int BM, int BN = GBN> constexpr size_t lds_bytes()
-{
-    return Tile<BM, BN>::STAGES * Tile<BM, BN>::STAGE_BYTES + sizeof(GroupTable) + 2 * GMAX_THREADS * sizeof(int);
-}
-static_assert(lds_bytes<32>() <= 163840 && lds_bytes<32, 128>() <= 163840 && lds_bytes<128>() <= 163840 &&
-                  lds_bytes<256>() <= 163840,
-              "LDS budget of a gfx950 workgroup");
-
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
 // Both are cached per device in atomics, so concurrent first calls and several GPUs are safe (a
@@ -1175,7 +1237,7 @@ template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s
     const int grid = (num_cus(dev) + 7) / 8 * 8;
     if (a.M <= 48 * a.L) {
         static std::atomic<bool> done[G_MAX_DEVICES];
-        const size_t lds = lds_bytes<32, small_bn(32, EPI)>();
+        const size_t lds = G_LDS_SMALL_BYTES;
         hipError_t e = set_lds(gmm_kernel_small<DT, EPI>, lds, dev, done);
         if (e != hipSuccess)
             return e;
@@ -1184,7 +1246,7 @@ template <int DT, int EPI> static hipError_t launch_one(GmmArgs a, hipStream_t s
     }
     a.allow256 = a.M >= G_HEAVY_ROWS;  // some expert may reach the 256-row tile class
     static std::atomic<bool> done[G_MAX_DEVICES];
-    const size_t lds = std::max(std::max(lds_bytes<128>(), lds_bytes<256>()), lds_bytes<32>());
+    const size_t lds = G_LDS_BIG_BYTES;
     hipError_t e = set_lds(gmm_kernel_big<DT, EPI>, lds, dev, done);
     if (e != hipSuccess)
         return e;
@@ -1216,6 +1278,22 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
     }
     return hipErrorInvalidValue;
 }
+
+#ifdef CAM_GMM_TIMELINE
+}  // namespace cam
+// diagnostic build only: copy the per-tile records out and clear them
+extern "C" __attribute__((visibility("default"))) int camhipDebugGmmTimeline(void *host_dst, size_t bytes)
+{
+    const size_t n = std::min(bytes, sizeof(cam::g_cam_tl));
+    if (hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(cam::g_cam_tl), n, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    static uint8_t zeros[sizeof(cam::g_cam_tl)];
+    return hipMemcpyToSymbol(HIP_SYMBOL(cam::g_cam_tl), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice) == hipSuccess
+               ? (int)(n / sizeof(cam::g_cam_tl[0]))
+               : -1;
+}
+namespace cam {
+#endif
 
 // Per-token int8 requantisation of h (post_swiglu_dynamic_quant.h:164-231): one block per row.
 __global__ __launch_bounds__(256) void quant_rows_int8_kernel(const float *__restrict__ h,
