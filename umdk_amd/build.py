@@ -1,6 +1,7 @@
 """Builds libcamhip.so (the C-ABI library of HIP kernels for gfx950) in-tree.
 
-    python -m umdk_amd.build          # -> umdk_amd/lib/libcamhip.so
+    python -m umdk_amd.build              # -> umdk_amd/lib/libcamhip.so
+    python -m umdk_amd.build --timeline   # diagnostic variant -> umdk_amd/lib/timeline/libcamhip.so
 
 Every source is compiled by hipcc for gfx950 only; symbols are hidden except
 the extern "C" entry points declared in include/camhip.h.
@@ -30,9 +31,9 @@ def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, src + ".o")
-    cmd = [HIPCC] + COMMON + ["-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src, defines=(), build_dir=BUILD):
+    obj = os.path.join(build_dir, src + ".o")
+    cmd = [HIPCC] + COMMON + list(defines) + ["-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -44,22 +45,32 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
-    os.makedirs(BUILD, exist_ok=True)
-    os.makedirs(LIBDIR, exist_ok=True)
+def build(verbose=True, defines=(), lib=LIB):
+    """Compile every source and link `lib`.  `defines` (e.g. ["-DCAM_GMM_TIMELINE"]) build a variant,
+    with its objects in a build folder of its own."""
+    build_dir = BUILD if not defines else os.path.join(BUILD, "variant_" + "_".join(d.lstrip("-D") for d in defines))
+    os.makedirs(build_dir, exist_ok=True)
+    os.makedirs(os.path.dirname(lib), exist_ok=True)
     srcs = sources()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda f: _compile(f, defines, build_dir), srcs))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
+
+
+# the diagnostic build of the grouped GEMMs' per-tile timeline (umdk_amd/timeline.py); never the shipped library
+TIMELINE_LIB = os.path.join(LIBDIR, "timeline", "libcamhip.so")
 
 
 if __name__ == "__main__":
-    build()
+    if "--timeline" in sys.argv[1:]:
+        build(defines=["-DCAM_GMM_TIMELINE"], lib=TIMELINE_LIB)
+    else:
+        build()
