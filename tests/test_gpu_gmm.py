@@ -248,6 +248,15 @@ def test_gmm_mixed_tile_heights_many_heavy_tiles(ops, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("counts", [[700, 200, 0, 450], [700, 5, 1100, 30], [2100, 100, 2100], [2100, 7, 2100, 1]])
+def test_gmm_heavy_tiles_with_one_light_class(ops, dtype, counts):
+    # heavy experts next to only 128-row or only 32-row experts (the other class has no tiles and is skipped),
+    # with fewer heavy tiles than blocks (first two) and with more (last two, I = 2048: 16 N-tiles per M-tile)
+    print(f"counts {counts} {dtype}", flush=True)
+    _ragged_vs_torch(ops, counts, 4096, 2048 if max(counts) > 2000 else 256, dtype, 3, 29)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
 def test_gmm_mixed_tile_heights_short_reduction(ops, dtype):
     # H = 1024 (fewer than 32 k-steps): every expert takes the 128-row tile, whatever its rows
     _ragged_vs_torch(ops, [700, 5, 1100, 30, 400, 0, 200, 383], 1024, 256, dtype, 7, 28)
