@@ -415,26 +415,24 @@ camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(const float *logits, const
     const int cap = (int)recvRowsCapacity;
     const int tpc = cam::route_tokens_per_block();
     const int nc = (T + tpc - 1) / tpc;
-    // workspace: chunk counts -> chunk bases [L][nc], send offsets [L], expert totals [L], the arrival count,
+    // workspace: chunk counts -> chunk bases [L][nc], chunk prefixes over the experts [L][nc], send offsets [L],
     // the in-chunk ranks [T][K]
     const uint64_t counts_bytes = ((uint64_t)L * nc * sizeof(int32_t) + 255) & ~(uint64_t)255;
     const uint64_t vec_bytes = ((uint64_t)L * sizeof(int32_t) + 255) & ~(uint64_t)255;
-    const uint64_t rank_off = counts_bytes + 2 * vec_bytes + 256;
+    const uint64_t rank_off = 2 * counts_bytes + vec_bytes;
     const uint64_t ws = rank_off + (uint64_t)T * K * sizeof(int32_t);
     return make_executor(
         ws,
         [=](void *w, hipStream_t s) {
             int32_t *counts = (int32_t *)w;
-            int32_t *send_off = (int32_t *)((uint8_t *)w + counts_bytes);
-            int32_t *totals = (int32_t *)((uint8_t *)w + counts_bytes + vec_bytes);
-            uint32_t *arrivals = (uint32_t *)((uint8_t *)w + counts_bytes + 2 * vec_bytes);
+            int32_t *pref = (int32_t *)((uint8_t *)w + counts_bytes);
+            int32_t *send_off = (int32_t *)((uint8_t *)w + 2 * counts_bytes);
             int32_t *chunk_rank = (int32_t *)((uint8_t *)w + rank_off);
-            hipError_t e = cam::launch_route_hist(logits, bias, T, E, K, L, topkIdx, topkWeights, counts, arrivals,
+            hipError_t e = cam::launch_route_hist(logits, bias, T, E, K, L, topkIdx, topkWeights, counts, pref,
                                                   chunk_rank, s);
             if (e != hipSuccess)
                 return e;
-            e = cam::launch_scan_notify(L, nc, counts, totals, arrivals, send_off, recvCount, recvTokensPerExpert,
-                                        s);
+            e = cam::launch_scan_notify(L, nc, counts, pref, send_off, recvCount, recvTokensPerExpert, s);
             if (e != hipSuccess)
                 return e;
             return cam::launch_dispatch(x, topkIdx, send_off, nullptr, T, H, K, L, 0, cap, q, recvX, recvXScales,

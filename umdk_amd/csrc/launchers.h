@@ -15,12 +15,12 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
                         float *topk_w, hipStream_t s, int64_t *topk_idx64 = nullptr);
 
 // routing that also writes per-chunk histograms of the ids below Ec: chunks of route_tokens_per_block() tokens,
-// chunk_counts[e * nc + c], and each such pick's rank among its chunk's picks of the same expert,
-// chunk_rank[t * K + k] (the prefill step)
+// chunk_counts[e * nc + c], each chunk's exclusive prefix of its histogram over the experts, chunk_pref[e * nc +
+// c], and each such pick's rank among its chunk's picks of the same expert, chunk_rank[t * K + k] (the prefill
+// step)
 int route_tokens_per_block();
-// (*arrivals is cleared for the launch_scan_notify that follows)
 hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
-                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, int32_t *chunk_rank,
+                             float *topk_w, int32_t *chunk_counts, int32_t *chunk_pref, int32_t *chunk_rank,
                              hipStream_t s);
 
 // ---- dispatch layout (layout.hip)
@@ -33,10 +33,10 @@ size_t layout_workspace_bytes(int T, int K, int E, int R);
 hipError_t launch_layout(const int64_t *topk_idx, int T, int K, int E, int R, int32_t *ntok_per_rank,
                          int32_t *ntok_per_expert, int32_t *is_token_in_rank, int32_t *send_token_idx,
                          void *ws, hipStream_t s);
-// the prefill step: chunk counts [E][nc] -> exclusive chunk bases in place, row totals [E], then the one-rank
-// count exchange (run by the last block to arrive; *arrivals must be 0 at launch)
-hipError_t launch_scan_notify(int E, int nc, int32_t *counts, int32_t *totals, uint32_t *arrivals,
-                              int32_t *send_offset, int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s);
+// the prefill step: chunk counts [E][nc] -> exclusive chunk bases in place, and the one-rank count exchange from
+// the row totals and the summed chunk prefixes [E][nc] of launch_route_hist
+hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pref, int32_t *send_offset,
+                              int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s);
 // int32 topk ids, used by the fused path
 hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
                              int32_t *send_token_idx, void *ws, hipStream_t s);

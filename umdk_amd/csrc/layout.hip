@@ -188,102 +188,76 @@ __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *_
     }
 }
 
-// The prefill step's bookkeeping after route_kernel<.., HIST> (chunks of 16 tokens): each local expert's
-// row of chunk counts is scanned in place into exclusive chunk bases by one wave (four rows per block, all
-// blocks in parallel: a single block would be bound by one CU's outstanding memory requests), each row's
-// total goes to `totals`, and the last block to finish (an atomic arrival count, cleared by the routing
-// launch) runs the one-rank count exchange over the totals: send_offset = exclusive, recv_count =
-// inclusive prefix over the experts, tokens_per_expert as int64.
+// The prefill step's bookkeeping after route_kernel<.., HIST> (chunks of 16 tokens): one wave per local
+// expert (four per block, all blocks in parallel: a single block would be bound by one CU's outstanding
+// memory requests) scans the expert's row of chunk counts in place into exclusive chunk bases, and sums the
+// expert's row of chunk prefixes (each chunk's count of the lower experts' picks) into its send offset, so
+// every expert's count exchange entry is known without a second pass over the totals: send_offset =
+// exclusive, recv_count = inclusive prefix over the experts, tokens_per_expert as int64.
 constexpr int SN_THREADS = 256;
 constexpr int SN_WAVES = SN_THREADS / 64;
 __global__ __launch_bounds__(SN_THREADS) void scan_notify_kernel(int E, int nc, int32_t *__restrict__ counts,
-                                                                 int32_t *__restrict__ totals,
-                                                                 uint32_t *__restrict__ arrivals,
+                                                                 const int32_t *__restrict__ pref,
                                                                  int32_t *__restrict__ send_offset,
                                                                  int32_t *__restrict__ recv_count,
                                                                  int64_t *__restrict__ tokens_per_expert)
 {
-    __shared__ int32_t wsum[SN_WAVES];
-    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int e = blockIdx.x * SN_WAVES + w;
-    if (e < E) {
-        int32_t *row = counts + (size_t)e * nc;
-        int32_t pre[4];  // the first 256 chunks' counts in flight together
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            pre[u] = u * 64 + lane < nc ? row[u * 64 + lane] : 0;
-        int32_t carry = 0;
-        for (int c0 = 0; c0 < nc; c0 += 64) {
-            const int c = c0 + lane;
-            int32_t v = 0;
-            if (c0 < 256) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    v = c0 == u * 64 ? pre[u] : v;
-            } else {
-                v = c < nc ? row[c] : 0;
-            }
-            int32_t incl = v;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int32_t u = __shfl_up(incl, o, 64);
-                if (lane >= o)
-                    incl += u;
-            }
-            if (c < nc)
-                row[c] = carry + incl - v;
-            carry += __shfl(incl, 63, 64);
-        }
-        if (lane == 0)
-            totals[e] = carry;
-    }
-    // publish this block's totals (release at agent scope), then count the block in; the last block to arrive
-    // acquires every block's totals
-    __threadfence();
-    __syncthreads();
-    if (tid == 0)
-        last = atomicAdd(arrivals, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last)
+    if (e >= E)
         return;
-    __threadfence();
-    int32_t carry = 0;  // running total of the earlier groups of SN_THREADS experts
-    for (int e0 = 0; e0 < E; e0 += SN_THREADS) {
-        const int q = e0 + tid;
-        const int32_t c = q < E ? __hip_atomic_load(totals + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        int32_t v = c;
+    int32_t *row = counts + (size_t)e * nc;
+    const int32_t *prow = pref + (size_t)e * nc;
+    int32_t pre[4], pp[4];  // the first 256 chunks' counts and prefixes in flight together
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const bool in = u * 64 + lane < nc;
+        pre[u] = in ? row[u * 64 + lane] : 0;
+        pp[u] = in ? prow[u * 64 + lane] : 0;
+    }
+    int32_t carry = 0, below = 0;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int c = c0 + lane;
+        int32_t v = 0, b = 0;
+        if (c0 < 256) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v = c0 == u * 64 ? pre[u] : v;
+                b = c0 == u * 64 ? pp[u] : b;
+            }
+        } else if (c < nc) {
+            v = row[c];
+            b = prow[c];
+        }
+        int32_t incl = v;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const int32_t u = __shfl_up(v, o, 64);
+            const int32_t u = __shfl_up(incl, o, 64);
             if (lane >= o)
-                v += u;
+                incl += u;
         }
-        if (lane == 63)
-            wsum[w] = v;
-        __syncthreads();
-        int32_t before = carry;
-        for (int ww = 0; ww < w; ++ww)
-            before += wsum[ww];
-        const int32_t incl = before + v;
-        if (q < E) {
-            send_offset[q] = incl - c;
-            recv_count[q] = incl;
-            tokens_per_expert[q] = c;
-        }
-        for (int ww = 0; ww < SN_WAVES; ++ww)
-            carry += wsum[ww];
-        __syncthreads();  // wsum is rewritten by the next group
+        if (c < nc)
+            row[c] = carry + incl - v;
+        carry += __shfl(incl, 63, 64);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            b += __shfl_xor(b, o, 64);
+        below += b;
+    }
+    if (lane == 0) {
+        send_offset[e] = below;
+        recv_count[e] = below + carry;
+        tokens_per_expert[e] = carry;
     }
 }
 
-hipError_t launch_scan_notify(int E, int nc, int32_t *counts, int32_t *totals, uint32_t *arrivals,
-                              int32_t *send_offset, int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s)
+hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pref, int32_t *send_offset,
+                              int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s)
 {
     if (E < 1 || E > MAX_E || nc < 1)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(scan_notify_kernel, dim3((E + SN_WAVES - 1) / SN_WAVES), dim3(SN_THREADS), 0, s, E, nc,
-                       counts, totals, arrivals, send_offset, recv_count, tokens_per_expert);
+                       counts, pref, send_offset, recv_count, tokens_per_expert);
     return hipGetLastError();
 }
 

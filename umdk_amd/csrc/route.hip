@@ -47,7 +47,10 @@ __device__ __forceinline__ uint32_t order_key(float s)
 }
 
 // HIST: the block's 16 tokens are one layout chunk; it also writes the chunk's histogram of the picked
-// ids below Ec (the local experts), chunk_counts[e * gridDim.x + blockIdx.x] for every e < Ec, and each such
+// ids below Ec (the local experts), chunk_counts[e * gridDim.x + blockIdx.x] for every e < Ec, the chunk's
+// exclusive prefix of that histogram over the experts, chunk_pref[e * gridDim.x + blockIdx.x] (summed over the
+// chunks it is expert e's offset among the received rows, so no step after this launch needs every expert's
+// total), and each such
 // pick's rank among the chunk's picks of the same expert in (t,k) order, chunk_rank[t * K + k].  A token's K
 // picks are distinct experts, so that rank is the number of earlier tokens of the chunk that picked the
 // expert: each expert gets a 16-bit mask of the chunk's tokens that picked it (an LDS atomic OR, which no
@@ -60,7 +63,7 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
                                                                  float *__restrict__ topk_w,
                                                                  int64_t *__restrict__ topk_idx64,
                                                                  int Ec = 0, int32_t *__restrict__ chunk_counts = nullptr,
-                                                                 uint32_t *__restrict__ arrivals = nullptr,
+                                                                 int32_t *__restrict__ chunk_pref = nullptr,
                                                                  int32_t *__restrict__ chunk_rank = nullptr)
 {
     const int lane = threadIdx.x & 63;
@@ -135,8 +138,6 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
     }
     if constexpr (HIST) {
         static_assert(ROUTE_WAVES * 4 <= 32, "a chunk's tokens fit a 32-bit mask");
-        if (blockIdx.x == 0 && threadIdx.x == 0)
-            *arrivals = 0u;  // the arrival count of the scan launch that follows on the stream
         __shared__ uint32_t picked[ROUTE_MAX_PER_LANE * 16];  // per expert: the chunk's tokens that picked it
         for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
             picked[e] = 0u;
@@ -148,8 +149,38 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
         __syncthreads();
         if (local)
             chunk_rank[(size_t)t * K + l16] = __popc(picked[my_idx] & ((1u << tl) - 1u));
-        for (int e = threadIdx.x; e < Ec; e += ROUTE_WAVES * 64)
-            chunk_counts[(size_t)e * gridDim.x + blockIdx.x] = __popc(picked[e]);
+        // the histogram, and its exclusive prefix over the experts: thread i owns experts [i PE, (i + 1) PE)
+        constexpr int NT = ROUTE_WAVES * 64, PE = (ROUTE_MAX_PER_LANE * 16 + NT - 1) / NT;
+        __shared__ int32_t wsum[ROUTE_WAVES];
+        int cnt[PE], own = 0;
+#pragma unroll
+        for (int q = 0; q < PE; ++q) {
+            const int e = threadIdx.x * PE + q;
+            cnt[q] = e < Ec ? __popc(picked[e]) : 0;
+            own += cnt[q];
+        }
+        int incl = own;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(incl, o, 64);
+            if (lane >= o)
+                incl += u;
+        }
+        if (lane == 63)
+            wsum[threadIdx.x >> 6] = incl;
+        __syncthreads();
+        int run = incl - own;
+        for (int v = 0; v < (int)(threadIdx.x >> 6); ++v)
+            run += wsum[v];
+#pragma unroll
+        for (int q = 0; q < PE; ++q) {
+            const int e = threadIdx.x * PE + q;
+            if (e < Ec) {
+                chunk_counts[(size_t)e * gridDim.x + blockIdx.x] = cnt[q];
+                chunk_pref[(size_t)e * gridDim.x + blockIdx.x] = run;
+            }
+            run += cnt[q];
+        }
     }
 }
 
@@ -182,7 +213,7 @@ hipError_t launch_route(const float *logits, const float *bias, int T, int E, in
 int route_tokens_per_block() { return ROUTE_WAVES * 4; }
 
 hipError_t launch_route_hist(const float *logits, const float *bias, int T, int E, int K, int Ec, int32_t *topk_idx,
-                             float *topk_w, int32_t *chunk_counts, uint32_t *arrivals, int32_t *chunk_rank,
+                             float *topk_w, int32_t *chunk_counts, int32_t *chunk_pref, int32_t *chunk_rank,
                              hipStream_t s)
 {
     if (T == 0)
@@ -194,7 +225,7 @@ hipError_t launch_route_hist(const float *logits, const float *bias, int T, int 
     const int per = (E + 15) >> 4;
 #define ROUTE_HIST_CASE(P)                                                                                          \
     hipLaunchKernelGGL((route_kernel<P, true>), g, b, 0, s, logits, bias, T, E, K, topk_idx, topk_w, nullptr, Ec,   \
-                       chunk_counts, arrivals, chunk_rank)
+                       chunk_counts, chunk_pref, chunk_rank)
     if (per <= 1)
         ROUTE_HIST_CASE(1);
     else if (per <= 2)
