@@ -272,6 +272,37 @@ CAMHIP_API camhipStatus camhipGroupedMatmulGetWorkspaceSize(const void *x, const
 CAMHIP_API camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                             void *stream);
 
+/* Both expert GEMMs of a layer in one call (extension, no reference counterpart; the reference runs them
+ * as two workspace-linked stages inside its fused op, grouped_matmul_slice_m_per_token_dequant_swiglu_quant_
+ * multistage_workspace.h:386-401 waiting per group on the first stage's flags): GMM1 + SwiGLU exactly as
+ * camhipGroupedMatmulSwiglu with n = gmm1HiddenSize (fp8: h requantised to fp8 1x128, hScale k-major
+ * [I/128, m]; bf16: h bf16), then GMM2 exactly as camhipGroupedMatmul on h -> out [m, hidden] bf16.  The
+ * results are bit-identical to those two calls.  Where a chained kernel exists (decode-sized groups, at most
+ * 48 rows per group on average) the two run as one launch in which each GMM2 tile waits for the GMM1 tiles
+ * of its rows; the workspace then holds the readiness counters, cleared by this call.  dtype 0 (bf16) or
+ * 3 (fp8); int8 is not accepted (use the two calls).  If a wait in the chained launch outlasts its bound
+ * (2 s, which only a GPU shared with other work that keeps blocks of the launch from running could cause),
+ * the launch ends with unspecified outputs and sets the device's sync status (camhipGetSyncStatus). */
+CAMHIP_API camhipStatus camhipMoeExpertsGetWorkspaceSize(const void *x, const float *xScale,
+                                                         const int64_t *groupList, int64_t numGroups, int64_t m,
+                                                         int64_t hidden, int64_t gmm1HiddenSize,
+                                                         const void *gmm1Weight, const float *gmm1WeightScale,
+                                                         const void *gmm2Weight, const float *gmm2WeightScale,
+                                                         int64_t dtype, int64_t xScaleLayout, void *h, float *hScale,
+                                                         uint16_t *out, uint64_t *workspaceSize,
+                                                         camhipExecutor **executor);
+CAMHIP_API camhipStatus camhipMoeExperts(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
+                                         void *stream);
+
+/* Sync status of the current device's chained GEMM launches (camhipMoeExperts, camhipFusedDeepMoe):
+ * *status = 0, or nonzero once a readiness wait gave up (sticky; clear != 0 resets it).  Synchronous:
+ * call it after the launches in question have completed (extension, no reference counterpart). */
+CAMHIP_API camhipStatus camhipGetSyncStatus(int32_t *status, int32_t clear);
+/* Test hook (extension): waitTicks > 0 sets the chained launches' wait bound in 100 MHz constant-clock
+ * ticks (<= 0 restores 2 s); unreachable != 0 makes every wait unreachable, so that each one gives up at
+ * the bound.  Applies to launches issued after the call, from any thread. */
+CAMHIP_API void camhipDebugSetSyncWait(int64_t waitTicks, int32_t unreachable);
+
 /* ------------------------------------------------------------------ fused decode entry
  * Replaces aclnnFusedDeepMoe (fused_deep_moe/op_api/aclnn_fused_deep_moe.h:19-50;
  * binding pybind/fused_deep_moe.cpp:30-83): dispatch + GMM1 + SwiGLU + GMM2 +

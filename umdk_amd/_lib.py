@@ -29,6 +29,7 @@ SIGNATURES = {
     "camhipFusedDeepMoe": "pppppp p pppp ppp iiiiii iiiii ppp",
     "camhipMoePrefillDispatch": "ppp iiiiiii pppppppp",
     "camhipMoePrefillCombine": "ppppp iiiii p",
+    "camhipMoeExperts": "ppp iiii pppp ii ppp",
 }
 
 _lib = None
@@ -61,6 +62,10 @@ def lib():
         # outputs, then the stream
         L.camhipMoeCombineNormalNoAlloc.restype = ctypes.c_int
         L.camhipMoeCombineNormalNoAlloc.argtypes = [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P]
+        L.camhipGetSyncStatus.restype = ctypes.c_int
+        L.camhipGetSyncStatus.argtypes = [ctypes.POINTER(ctypes.c_int32), ctypes.c_int32]
+        L.camhipDebugSetSyncWait.restype = None
+        L.camhipDebugSetSyncWait.argtypes = [_I, ctypes.c_int32]
         _lib = L
     return _lib
 
@@ -117,6 +122,17 @@ def launch(name, *args, workspace=None, stream=None, device=None):
     st = getattr(L, name)(workspace.data_ptr() if workspace is not None else None, have, ex, stream)
     if st != 0:
         raise CamHipError(f"{name} failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+
+
+def sync_status(clear=False):
+    """The current device's sync status of the chained GEMM launches (0: no readiness wait gave up);
+    synchronous, call after the launches have completed."""
+    L = lib()
+    v = ctypes.c_int32(0)
+    st = L.camhipGetSyncStatus(ctypes.byref(v), 1 if clear else 0)
+    if st != 0:
+        raise CamHipError(f"camhipGetSyncStatus failed ({st}): {L.camhipGetLastErrorMsg().decode()}")
+    return v.value
 
 
 def workspace_size(name, *args):

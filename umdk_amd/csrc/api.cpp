@@ -634,4 +634,82 @@ camhipStatus camhipGroupedMatmul(void *workspace, uint64_t workspaceSize, camhip
     return run_executor("grouped_matmul", workspace, workspaceSize, executor, stream);
 }
 
+// ---------------------------------------------------------------- experts: GMM1 + SwiGLU -> GMM2
+camhipStatus camhipMoeExpertsGetWorkspaceSize(const void *x, const float *xScale, const int64_t *groupList,
+                                              int64_t numGroups, int64_t m, int64_t hidden, int64_t gmm1HiddenSize,
+                                              const void *gmm1Weight, const float *gmm1WeightScale,
+                                              const void *gmm2Weight, const float *gmm2WeightScale, int64_t dtype,
+                                              int64_t xScaleLayout, void *h, float *hScale, uint16_t *out,
+                                              uint64_t *workspaceSize, camhipExecutor **executor)
+{
+    CHECK_PARAM(dtype == CAMHIP_DTYPE_BF16 || dtype == CAMHIP_DTYPE_FP8,
+                "moe_experts: dtype %lld not supported (0 bf16 or 3 fp8; int8 runs the two grouped-matmul calls)",
+                (long long)dtype);
+    camhipStatus st = check_gmm("moe_experts", x, xScale, groupList, numGroups, m, hidden, gmm1HiddenSize,
+                                gmm1Weight, gmm1WeightScale, dtype, true);
+    if (st != CAMHIP_SUCCESS)
+        return st;
+    st = check_gmm("moe_experts", h, dtype == CAMHIP_DTYPE_FP8 ? hScale : nullptr, groupList, numGroups, m,
+                   gmm1HiddenSize / 2, hidden, gmm2Weight, gmm2WeightScale, dtype, false);
+    if (dtype == CAMHIP_DTYPE_BF16 && st == CAMHIP_SUCCESS)
+        CHECK_PTR(h);
+    if (st != CAMHIP_SUCCESS)
+        return st;
+    CHECK_PTR(out);
+    CHECK_PARAM(xScaleLayout == 0 || xScaleLayout == 1, "moe_experts: xScaleLayout %lld must be 0 or 1",
+                (long long)xScaleLayout);
+    const int L = (int)numGroups, M = (int)m, H = (int)hidden, N1 = (int)gmm1HiddenSize, dt = (int)dtype;
+    const int epi1 = dt == cam::DT_FP8 ? cam::EPI_SWIGLU_FP8 : cam::EPI_SWIGLU_BF16;
+    const cam::GmmArgs g1{(const uint8_t *)x, xScale, groupList, L, M, H, N1, (const uint8_t *)gmm1Weight,
+                          gmm1WeightScale, (uint8_t *)h, hScale};
+    const cam::GmmArgs g2{(const uint8_t *)h, dt == cam::DT_FP8 ? hScale : nullptr, groupList, L, M, N1 / 2, H,
+                          (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)out, nullptr};
+    const bool chained = cam::gmm_chain_supported(g1, g2, dt);
+    // workspace: the readiness counters (chained), then the k-major copy of row-major fp8 scales
+    const uint64_t ready_bytes = chained ? ((uint64_t)cam::gmm_chain_counters(M, L) * 4 + 255) & ~(uint64_t)255 : 0;
+    const bool transpose = dt == cam::DT_FP8 && xScaleLayout == 0;
+    const int nb = H / 128;
+    const uint64_t ws = ready_bytes + (transpose ? (uint64_t)M * nb * 4 : 0);
+    return make_executor(
+        ws,
+        [=](void *w, hipStream_t s) {
+            cam::GmmArgs a = g1;
+            hipError_t e = hipSuccess;
+            if (transpose) {
+                float *ks = (float *)((uint8_t *)w + ready_bytes);
+                e = cam::launch_scales_to_kmajor(g1.As, groupList, L, M, nb, ks, s);
+                if (e != hipSuccess)
+                    return e;
+                a.As = ks;
+            }
+            if (!chained) {
+                e = cam::launch_gmm(a, dt, epi1, s);
+                return e != hipSuccess ? e : cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s);
+            }
+            int32_t *ready = (int32_t *)w;
+            e = cam::launch_fill_i32(ready, 0, cam::gmm_chain_counters(M, L), s);
+            return e != hipSuccess ? e : cam::launch_gmm_chain(a, g2, dt, ready, s);
+        },
+        workspaceSize, executor);
+}
+
+camhipStatus camhipMoeExperts(void *workspace, uint64_t workspaceSize, camhipExecutor *executor, void *stream)
+{
+    return run_executor("moe_experts", workspace, workspaceSize, executor, stream);
+}
+
+camhipStatus camhipGetSyncStatus(int32_t *status, int32_t clear)
+{
+    CHECK_PTR(status);
+    int v = 0;
+    hipError_t e = cam::sync_status_read(&v, clear != 0);
+    if (e != hipSuccess)
+        return fail(CAMHIP_ERROR_RUNTIME, "get_sync_status: %s", hipGetErrorString(e));
+    *status = v;
+    g_last_error.clear();
+    return CAMHIP_SUCCESS;
+}
+
+void camhipDebugSetSyncWait(int64_t waitTicks, int32_t unreachable) { cam::sync_debug_set(waitTicks, unreachable); }
+
 }  // extern "C"

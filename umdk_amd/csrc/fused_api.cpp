@@ -5,7 +5,9 @@
 //   exchange -> quantised dispatch -> GMM1+SwiGLU -> GMM2 -> combine,
 //   plus the optional shared expert on all tokens.  At decode sizes
 //   (batch*topk <= 8192) the first three stages are one single-block launch,
-//   and dispatch writes the combine's row map: five launches in all.
+//   dispatch writes the combine's row map, and GMM1 and GMM2 run as one
+//   chained launch (fp8, bf16; each GMM2 tile waits for the GMM1 tiles of its
+//   rows): four launches in all.
 // Every intermediate lives in the caller's workspace and every size is fixed
 // by (batch, topk): no host synchronisation and no allocation, so the call can
 // be captured in a HIP graph (the reference's fused op is its graph-capturable
@@ -44,7 +46,7 @@ struct Carve {
 };
 
 struct FusedLayout {
-    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv, hf, amax;
+    uint64_t ids, layout_ws, counts, send_off, recv_cnt, total, sti, ex, xs, eidx, h, hs, y, inv, hf, amax, ready;
     uint64_t sh_x, sh_xs, sh_h, sh_hs, sh_gl, sh_hf, sh_amax;
     uint64_t bytes;
 };
@@ -78,6 +80,7 @@ FusedLayout plan_fused(int T, int H, int K, int L, int I, int Ish, int dt, bool 
     f.inv = c.take(4 * N);
     f.hf = c.take(int8 ? N * I * 4 : 0);  // int8: fp32 h and its row maxima before the requantisation
     f.amax = c.take(int8 ? N * (I / cam::GMM_AMAX_COLS) * 4 : 0);  // partial row maxima of h
+    f.ready = c.take(int8 ? 0 : 4 * (uint64_t)cam::gmm_chain_counters((int)N, L));  // chained GEMMs' counters
     if (shared) {
         f.sh_x = c.take((uint64_t)T * H * esz);
         f.sh_xs = c.take((uint64_t)T * scale_bytes(dt, H));
@@ -216,11 +219,29 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         if (T == 0) {  // no tokens: no expert receives any
             return cam::launch_fill_i64(expertTokenNums, 0, L, s);
         }
+        cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
+                        (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
+        cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
+                        (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
+        if (wlist) {
+            g1.Wl = (const uint8_t *const *)gmm1Weight;
+            g1.Wsl = (const float *const *)gmm1WeightScale;
+            g2.Wl = (const uint8_t *const *)gmm2Weight;
+            g2.Wsl = (const float *const *)gmm2WeightScale;
+        }
+        // GMM1 -> GMM2 as one launch where a chained kernel exists; its readiness counters start at zero
+        const bool chained = cam::gmm_chain_supported(g1, g2, dt);
+        int32_t *ready = (int32_t *)P(f.ready);
+        const int nready = chained ? cam::gmm_chain_counters(N, L) : 0;
         if (N <= 8192) {
-            // decode sizes: id preparation, layout and count exchange in one launch
+            // decode sizes: id preparation, layout and count exchange in one launch (which also clears the
+            // counters)
             HIP_TRY(cam::launch_layout_small(expertIds, xActiveMask, T, K, L, ids, counts, (int32_t *)P(f.sti),
-                                             send_off, recv_cnt, (int32_t *)P(f.total), expertTokenNums, s));
+                                             send_off, recv_cnt, (int32_t *)P(f.total), expertTokenNums, s, ready,
+                                             nready));
         } else {
+            if (chained)
+                HIP_TRY(cam::launch_fill_i32(ready, 0, nready, s));
             HIP_TRY(cam::launch_prepare_ids(expertIds, xActiveMask, T, K, 0, L, ids, s));
             HIP_TRY(cam::launch_layout_i32(ids, T, K, L, counts, (int32_t *)P(f.sti), P(f.layout_ws), s));
             HIP_TRY(cam::launch_notify(counts, L, T, send_off, (int32_t *)P(f.total), recv_cnt, nullptr, nullptr,
@@ -231,20 +252,12 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
                                      (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv),
                                      expertSmoothScales, true));
-        cam::GmmArgs g1{(const uint8_t *)P(f.ex), (const float *)P(f.xs), expertTokenNums, L, N, H, 2 * I,
-                        (const uint8_t *)gmm1Weight, gmm1WeightScale, (uint8_t *)P(f.h), (float *)P(f.hs)};
-        if (wlist) {
-            g1.Wl = (const uint8_t *const *)gmm1Weight;
-            g1.Wsl = (const float *const *)gmm1WeightScale;
+        if (chained) {
+            HIP_TRY(cam::launch_gmm_chain(g1, g2, dt, ready, s));
+        } else {
+            HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), s));
+            HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
         }
-        HIP_TRY(gmm1(g1, (float *)P(f.hf), (float *)P(f.amax), s));
-        cam::GmmArgs g2{(const uint8_t *)P(f.h), (const float *)P(f.hs), expertTokenNums, L, N, I, H,
-                        (const uint8_t *)gmm2Weight, gmm2WeightScale, (uint8_t *)P(f.y), nullptr};
-        if (wlist) {
-            g2.Wl = (const uint8_t *const *)gmm2Weight;
-            g2.Wsl = (const float *const *)gmm2WeightScale;
-        }
-        HIP_TRY(cam::launch_gmm(g2, dt, cam::EPI_PLAIN, s));
         HIP_TRY(cam::launch_combine_gather((const uint16_t *)P(f.y), (const int32_t *)P(f.eidx), N,
                                            recv_cnt + (L - 1), expertScales, T, K, H, output,
                                            (const int32_t *)P(f.inv), s));

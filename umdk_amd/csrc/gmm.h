@@ -32,6 +32,24 @@ struct GmmArgs {
 };
 
 hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s);
+
+// GMM1 + SwiGLU and GMM2 in one persistent launch (fp8 with fp8 h, or bf16): every block runs its GMM1 tiles,
+// then its GMM2 tiles.  A GMM1 tile of (expert e, M-tile m) stores its h rows with agent-coherent stores and,
+// once they have completed, adds 1 to ready[m]; a GMM2 tile of m starts its DMAs only after ready[m] has
+// reached I/128 (every GMM1 tile of those rows).  ready holds gmm_chain_counters(M, L) zeroed ints (the
+// caller clears them before the launch).  A wait that does not complete within the wait bound gives up, sets
+// the device's sync status (sync_status_*) and the launch ends normally with unspecified outputs.
+// hipErrorNotSupported: this combination (int8, or GEMMs that would pick different row tiles) has no chained
+// kernel; run launch_gmm twice instead.  g1.C / g1.Cs are h and its k-major scales, g2.A / g2.As the same.
+int gmm_chain_counters(int M, int L);
+bool gmm_chain_supported(const GmmArgs &g1, const GmmArgs &g2, int dt);
+hipError_t launch_gmm_chain(const GmmArgs &g1, const GmmArgs &g2, int dt, int *ready, hipStream_t s);
+// Device sync status of the chained launches: nonzero once a readiness wait has given up (sticky until
+// cleared).  Synchronous: reads (and optionally clears) the current device's status word.
+hipError_t sync_status_read(int *status, bool clear);
+// Test hooks: the wait bound in constant-clock ticks (<= 0: the default, 2 s) and an unreachable target
+// (every wait gives up at the bound).
+void sync_debug_set(long long wait_ticks, int unreachable);
 // fp8 activation scales [M, nb] row-major -> [nb, M] k-major (the layout the GEMMs read: one k-step's
 // scales of consecutive rows are contiguous), rows [0, sum(group_list)) only.
 hipError_t launch_scales_to_kmajor(const float *src, const int64_t *group_list, int L, int M, int nb, float *dst,

@@ -114,6 +114,34 @@ struct ClassRanges {
     int lo[G_NCLASS], hi[G_NCLASS];
 };
 
+// Readiness between the two GEMMs of a chained launch (launch_gmm_chain): the GMM1 tiles of an M-tile
+// produce its h rows, the GMM2 tiles of that M-tile consume them.  Counters are indexed by M-tile over the
+// classes in turn (the 256-row M-tiles, then the 128-row ones, then the 32-row ones), the same in both GEMMs
+// because both split every expert into the same tile height.
+enum SyncRole { SYNC_NONE = 0, SYNC_PRODUCE = 1, SYNC_CONSUME = 2 };
+struct GmmSync {
+    int *ready;       // per M-tile: GMM1 tiles whose h rows have been stored
+    int target;       // GMM1 tiles per M-tile (I / 128); one more when a test makes every wait give up
+    long long ticks;  // wait bound in constant-clock ticks
+};
+// nonzero once a readiness wait has given up (sticky; read and cleared by the host, sync_status_read)
+__device__ int g_cam_sync_status;
+
+// h stores of a producing GMM1 tile: agent-coherent (sc1, written through to memory), so that a GMM2 tile on
+// another XCD, whose L2 has never held these lines during the launch, reads them from memory
+// (global address-space pointers: the atomics then need no aperture check of a flat address)
+template <typename T> __device__ __forceinline__ __attribute__((address_space(1))) T *gptr(T *p)
+{
+    return (__attribute__((address_space(1))) T *)p;
+}
+template <bool CO, typename T> __device__ __forceinline__ void st_h(T *p, T v)
+{
+    if constexpr (CO)
+        __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
 // Diagnostic build only (-DCAM_GMM_TIMELINE): every block records, per tile, its wall-clock start and end
 // (100 MHz constant clock) with the tile's class, expert and index, into 128 slots per block;
 // camhipDebugGmmTimeline copies them out.  Off in every product build.
@@ -246,6 +274,11 @@ __device__ __forceinline__ void dma4(const void *g, void *lds)
 {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
 }
+// agent-coherent (sc1): data another XCD may have written during the launch
+__device__ __forceinline__ void dma4_sc1(const void *g, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 16);
+}
 
 // The same DMAs through a buffer resource: the base sits in four SGPRs, the lane's 32-bit byte offset in one
 // VGPR and the k-step's offset in an SGPR, so a DMA needs no 64-bit address registers and no address
@@ -263,7 +296,9 @@ template <int BYTES, int AUX>
 __device__ __forceinline__ void bdma(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds)
 {
     auto *l = (__attribute__((address_space(3))) void *)lds;
-    if constexpr (BYTES == 4)
+    if constexpr (BYTES == 4 && AUX == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, voff, soff, 0, 16);
+    else if constexpr (BYTES == 4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, voff, soff, 0, 0);
     else if constexpr (AUX == 2)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, voff, soff, 0, 2);
@@ -289,9 +324,13 @@ __device__ __forceinline__ void lds_sync()
 // Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
 // (first < 0: balanced placement, see below), preceded by a run of rn tiles rs, rs + rstride, ... (an
 // increasing sequence: the first index past the class's tiles ends it).
-template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM)>
+// ROLE (chained launches only): SYNC_PRODUCE tiles store h agent-coherently and count each finished tile in
+// sy.ready; SYNC_CONSUME tiles start their DMAs only once sy.ready of their M-tile has reached sy.target.  Waves
+// beyond the tile's own (a 32-row class run by an 8-wave block) are spectators: they issue no DMA, MFMA or store
+// and only meet the block's barriers.
+template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM), int ROLE = SYNC_NONE>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gtab, int first, int rs = 0, int rn = 0,
-                                         int rstride = 1)
+                                         int rstride = 1, const GmmSync &sy = GmmSync{nullptr, 0, 0})
 {
     using TC = Tile<BM, small_bn(BM, EPI)>;
     constexpr int TBN = TC::BN;
@@ -310,6 +349,15 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = w / TC::WAVES_N, wn = w % TC::WAVES_N;
     const int l16 = lane & 15, lg = lane >> 4;
+    constexpr bool PRODUCE = ROLE == SYNC_PRODUCE, CONSUME = ROLE == SYNC_CONSUME;
+    const bool spect = ROLE != SYNC_NONE && w >= NW;
+    // M-tiles of the classes before this one (the readiness counters' index base)
+    int cls_base = 0;
+    if constexpr (ROLE != SYNC_NONE) {
+#pragma unroll
+        for (int k = 0; k < tile_class(BM); ++k)
+            cls_base += gtab->tile_end[k][p.L - 1];
+    }
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
     constexpr bool FP8 = DT == DT_FP8;
     constexpr bool INT8 = DT == DT_INT8;
@@ -350,6 +398,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         uint32_t ga[A_LOADS], gb[B_LOADS], gs[TC::S_DMAS];
         int wsg, wsu;  // fp8: weight-scale row offsets (gate / up n-blocks, or the wave's column block)
         int active;    // some row of this wave lies inside the segment (an int: a bool tail makes struct copies go through scratch)
+        int mti;       // readiness counter of the tile's M-tile (chained launches)
     };
     auto setup = [&](int tile, Ctx &c) {
         int lo = 0, hi = p.L - 1;
@@ -377,7 +426,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         c.n0 = SWIGLU ? nt * 128 : nt * TBN;  // first h-column (SwiGLU) or W row (plain)
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
         // DMA and meets every barrier): a tile of a short segment costs little more than its weights
-        c.active = c.row0 + wm * WM < c.seg1;
+        c.active = !spect && c.row0 + wm * WM < c.seg1;
+        if constexpr (ROLE != SYNC_NONE)
+            c.mti = cls_base + tile_prefix(e) + mt;
         if (p.Wl) {  // separated weights: one allocation per expert, pointers read by scalar loads (a vector
                      // load here would make the tile switch wait for every DMA in flight)
             c.wbase = reinterpret_cast<const uint8_t *>(
@@ -424,6 +475,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     // DMA instruction q (0 <= q < LOADS) of k-step kc of tile c into ring slot `slot`: A bands, then
     // W bands, then (fp8) the activation scales
     auto dma_one = [&](const Ctx &c, int kc, int slot, int q) {
+        if (spect)
+            return;
         uint8_t *st = smem + slot * STAGE_BYTES;
         if constexpr (CAM_GMM_BUFDMA && BM >= 128) {  // (the decode tile measured 0.4 us slower per step this way)
             if (q < A_LOADS) {
@@ -434,8 +487,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                                       st + A_BYTES + (i * NW + w) * 1024);
             } else {
                 const int d = q - A_LOADS - B_LOADS;
-                bdma<4, 0>(buf_rsrc(p.As), c.gs[d] * 4u, (uint32_t)kc * (uint32_t)p.M * 4u,
-                           st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+                bdma<4, CONSUME ? 16 : 0>(buf_rsrc(p.As), c.gs[d] * 4u, (uint32_t)kc * (uint32_t)p.M * 4u,
+                                          st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
             }
             return;
         }
@@ -452,7 +505,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 dma16(c.wbase + c.gb[i] + (uint32_t)kc * GKB, st + A_BYTES + (i * NW + w) * 1024);
         } else {
             const int d = q - A_LOADS - B_LOADS;
-            dma4(p.As + c.gs[d] + (size_t)kc * p.M, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            if constexpr (CONSUME)
+                dma4_sc1(p.As + c.gs[d] + (size_t)kc * p.M, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
+            else
+                dma4(p.As + c.gs[d] + (size_t)kc * p.M, st + A_BYTES + B_BYTES + w * TC::S_ROWS * 4 + d * 256);
         }
     };
 
@@ -478,6 +534,13 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     // ---- epilogue: lane holds rows m = row0 + wm*WM + 16 i + l16 and, per j, four
     // consecutive columns 16 j + 4 lg + q of the wave's WN-wide column range
     auto epilogue = [&](const Ctx &c) {
+        if (spect) {
+            if constexpr (EPI == EPI_SWIGLU_FP8) {
+                lds_sync();  // the two exchange barriers of the fp8 requantisation
+                lds_sync();
+            }
+            return;
+        }
         const int row0 = c.row0, seg1 = c.seg1, n0 = c.n0;
         if constexpr (EPI == EPI_PLAIN) {
 #pragma unroll
@@ -545,10 +608,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         reinterpret_cast<uint16_t *>(p.C) + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
 #pragma unroll
                     for (int j = 0; j < HF; ++j) {
-                        u32x2 v;
-                        v[0] = f32x2_to_bf16x2(h[i][j][0], h[i][j][1]);
-                        v[1] = f32x2_to_bf16x2(h[i][j][2], h[i][j][3]);
-                        *reinterpret_cast<u32x2 *>(hrow + 16 * j) = v;
+                        const uint64_t v = (uint64_t)f32x2_to_bf16x2(h[i][j][0], h[i][j][1]) |
+                                           ((uint64_t)f32x2_to_bf16x2(h[i][j][2], h[i][j][3]) << 32);
+                        st_h<PRODUCE>(reinterpret_cast<uint64_t *>(hrow + 16 * j), v);
                     }
                 }
             } else {
@@ -593,10 +655,11 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         uint8_t *hrow = p.C + (size_t)m * half_n + n0 + (WN / 2) * wn + 4 * lg;
 #pragma unroll
                         for (int j = 0; j < HF; ++j)
-                            *reinterpret_cast<uint32_t *>(hrow + 16 * j) = f32x4_to_e4m3(
-                                h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv, h[i][j][3] * inv);
+                            st_h<PRODUCE>(reinterpret_cast<uint32_t *>(hrow + 16 * j),
+                                          f32x4_to_e4m3(h[i][j][0] * inv, h[i][j][1] * inv, h[i][j][2] * inv,
+                                                        h[i][j][3] * inv));
                         if (wn == 0 && lg == 0)
-                            p.Cs[(size_t)(n0 / 128) * p.M + m] = amx[i] / 448.0f;  // k-major h scales
+                            st_h<PRODUCE>(p.Cs + (size_t)(n0 / 128) * p.M + m, amx[i] / 448.0f);  // k-major h scales
                     }
                 }
                 lds_sync();  // red is reused by the next tile
@@ -638,6 +701,59 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         }
     };
 
+    // ---- readiness (chained launches).  A producer counts a tile once every wave's h stores have completed:
+    // each wave's vmcnt wait that covers them, then a barrier, then one atomic add by thread 0.  A consumer
+    // wave polls the counter of the tile's M-tile (lane 0, agent-coherent load) before the tile's first DMA.
+    int sig = -1;      // producer: counter of the tile whose stores are still to be counted
+    int gave_up = 0;   // consumer: a wait of this wave gave up (the launch's outputs are void; no more waits)
+    auto signal = [&]() {
+        if constexpr (PRODUCE) {
+            if (sig >= 0 && threadIdx.x == 0)
+                __hip_atomic_fetch_add(gptr(sy.ready + sig), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sig = -1;
+        }
+    };
+    auto poll = [&](int m) -> int {
+        int v = 0;
+        if (lane == 0)
+            v = __hip_atomic_load(gptr(sy.ready + m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return __builtin_amdgcn_readfirstlane(v);
+    };
+    auto wait_ready = [&](int m) {
+        if constexpr (CONSUME) {
+            if (spect || gave_up)
+                return;
+            const uint64_t t0 = wall_clock64();
+            while (poll(m) < sy.target) {
+                if ((long long)(wall_clock64() - t0) > sy.ticks) {
+                    if (lane == 0)
+                        __hip_atomic_fetch_or(gptr(&g_cam_sync_status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    gave_up = 1;
+                    return;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+    };
+    // the M-tile counter of a tile index (the expert search of setup, nothing else)
+    auto mti_of = [&](int tile) {
+        int lo = 0, hi = p.L - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tile_end[mid - 1] * ntn <= tile)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        const int e = __builtin_amdgcn_readfirstlane(lo);
+        const int local = tile - tile_prefix(e) * ntn;
+        constexpr int GM = 8;
+        const int mt_e = tile_end[e] - tile_prefix(e);
+        const int grp = local / (GM * ntn), rem = local % (GM * ntn);
+        const int gm = min(GM, mt_e - grp * GM);
+        return cls_base + tile_prefix(e) + grp * GM + rem % gm;
+    };
+
     if constexpr (BM >= 256) {
         // 256-row tile (8 waves of 128 x 64; fp8, bf16 or int8): half the L2->LDS bytes per FLOP of the 128-row
         // tile.  Its accumulators leave no room for a second register set, so: two LDS stages, the
@@ -669,9 +785,20 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         CAM_TL_DECL
         if (tile < total) {
             setup(tile, c);
+            wait_ready(c.mti);
             prime(c);
         }
+        int next_ready = 0;  // consumer: the next tile's counter, polled while this tile's ring drains
         while (tile < total) {
+            if constexpr (PRODUCE) {
+                // the previous tile's h stores preceded this tile's first LOADS + B_LOADS DMAs (prime): once
+                // no more than those are in flight in any wave, the stores have completed
+                if (sig >= 0) {
+                    wait_vmcnt<LOADS + B_LOADS>();
+                    bar();
+                    signal();
+                }
+            }
             clear_acc();
             f32x4 pend[JF];
             float ps[JF];
@@ -789,10 +916,17 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                     for (int q = 0; q < 4; ++q)
                         acc[IF - 1][j][q] += pend[j][q] * ps[j];
             }
+            if constexpr (CONSUME) {
+                const int ntile = seq(kt + 1);
+                if (ntile < total && !gave_up && !spect)
+                    next_ready = poll(mti_of(ntile));  // answered while the ring drains
+            }
             wait_vmcnt<0>();  // the tail's reload has landed before the next tile reuses the ring
             bar();
             dequant_int8(c);
             epilogue(c);
+            if constexpr (PRODUCE)
+                sig = c.mti;
             CAM_TL_REC(c.e, tile);
             // int8: the dequantisation's loads have landed before the next tile (otherwise the compiler,
             // unsure of them, waits for every DMA in flight inside the k-loop)
@@ -801,8 +935,17 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             tile = seq(++kt);
             if (tile < total) {
                 setup(tile, c);
+                if constexpr (CONSUME) {
+                    if (next_ready < sy.target)
+                        wait_ready(c.mti);
+                }
                 prime(c);
             }
+        }
+        if constexpr (PRODUCE) {
+            wait_vmcnt<0>();
+            bar();
+            signal();
         }
         return;
     } else {
@@ -822,16 +965,23 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         CAM_TL_DECL
         int kb = 0;          // the block's k-steps before the current tile
         bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
+        int cur_ready = 0;    // consumer: the current tile's counter as polled before the previous tile's epilogue
+        // A consumer chains into its next tile only when that tile's rows are ready: wave 0 copies the
+        // counter into LDS by DMA at the tile's start, every wave reads it at k-step edge STAGES-2 (the copy
+        // has landed by then, as the producer's stores have), which precedes the first past-the-end DMA.
+        constexpr int SYNC_EDGE = GSTAGES - 2;
+        const bool can_chain = nk >= GSTAGES && (!CONSUME || nk >= SYNC_EDGE + GSTAGES);
         while (true) {
             const int ntile = seq(++kt);
             const bool has_next = ntile < total;
             // (int8 chains too: its dequantisation's vector loads then wait for the next tile's first DMAs,
             // which land meanwhile -- measured 8 us faster on the int8 decode step than draining first)
-            const bool chain = has_next && nk >= GSTAGES;
+            int chain = has_next && can_chain;
             if (has_next)
                 setup(ntile, nxt);
             else
                 nxt = cur;
+            bool poll_next = false;  // consumer: the next tile's counter is on its way into LDS
             auto slot = [&](int ks) { return (kb + ks) % GSTAGES; };
             auto stage_ptr = [&](int ks) { return smem + slot(ks) * STAGE_BYTES; };
             // DMA instruction q of the current tile's k-step ksx (ksx may run past the end)
@@ -852,19 +1002,51 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                     dma_ks(ksx, q);
             };
             if (!primed) {
+                if constexpr (CONSUME) {
+                    if (cur_ready < sy.target)
+                        wait_ready(cur.mti);
+                }
 #pragma unroll
                 for (int s0 = 0; s0 < GSTAGES; ++s0)
 #pragma unroll
                     for (int q = 0; q < LOADS; ++q)
                         dma_one(cur, min(s0, nk - 1), slot(s0), q);
             }
+            if constexpr (CONSUME) {
+                if (chain) {
+                    chain = 0;
+                    poll_next = true;
+                    if (w == 0)
+                        dma4_sc1(sy.ready + nxt.mti, scratch);
+                }
+            }
             wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
             bar();
+            // producer, unprimed tile: the previous tile's stores preceded these STAGES k-steps of DMAs
+            if constexpr (PRODUCE) {
+                if (!primed)
+                    signal();
+            }
             clear_acc();
             // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
+            int edge = 0;
             auto step_edge = [&]() {
                 wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
                 bar();
+                if constexpr (ROLE != SYNC_NONE) {
+                    // edge SYNC_EDGE: every op a wave issued before this tile's k-loop has completed (only
+                    // LOADS (STAGES - 2) may be in flight, all issued since): the previous tile's h stores
+                    // (producer, chained tile) and wave 0's copy of the next tile's counter (consumer)
+                    if (edge == SYNC_EDGE) {
+                        if constexpr (PRODUCE)
+                            signal();
+                        if constexpr (CONSUME) {
+                            if (poll_next)
+                                chain = scratch[0] >= sy.target;  // (bar() is a compiler memory barrier: read afresh)
+                        }
+                    }
+                    ++edge;
+                }
             };
 
             if constexpr (FP8) {
@@ -963,9 +1145,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         mm(w0, ks + 1, act);
                     }
                 };
-                if (TC::WAVES_M == 1 || cur.active)  // (one row-wave: a tile always has rows for it)
+                if (!spect && (TC::WAVES_M == 1 || cur.active))  // (one row-wave: a tile always has rows for it)
                     kloop(std::true_type{});
-                else if constexpr (TC::WAVES_M > 1)
+                else if constexpr (TC::WAVES_M > 1 || ROLE != SYNC_NONE)
                     kloop(std::false_type{});
 #pragma unroll
                 for (int j = 0; j < JF; ++j)  // the last row's pending results
@@ -1021,18 +1203,24 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         mm(r1, ks + GSTAGES, act);
                     }
                 };
-                if (TC::WAVES_M == 1 || cur.active)  // (one row-wave: a tile always has rows for it)
+                if (!spect && (TC::WAVES_M == 1 || cur.active))  // (one row-wave: a tile always has rows for it)
                     kloop(std::true_type{});
-                else if constexpr (TC::WAVES_M > 1)
+                else if constexpr (TC::WAVES_M > 1 || ROLE != SYNC_NONE)
                     kloop(std::false_type{});
             }
 
             dequant_int8(cur);
             if (!chain) {
+                if constexpr (CONSUME) {
+                    if (has_next && !gave_up && !spect)
+                        cur_ready = poll(nxt.mti);  // answered while the ring drains
+                }
                 wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
                 bar();
             }
             epilogue(cur);
+            if constexpr (PRODUCE)
+                sig = cur.mti;
             CAM_TL_REC(cur.e, tile);
             kb += nk;
             if (!has_next)
@@ -1042,6 +1230,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             cur = nxt;
         }
         wait_vmcnt<0>();  // every DMA has landed before the block exits
+        if constexpr (PRODUCE) {
+            bar();
+            signal();
+        }
     }
 }
 
@@ -1107,23 +1299,31 @@ constexpr int G_SMALL_ROWS = CAM_GMM_SMALL_ROWS;
 // load is skewed (a few experts with a thousand rows, many with a handful) gets tall tiles where they
 // halve the operand traffic and short ones where a tall tile would multiply padding.  The light experts'
 // (at most three M-tiles each) weights are fetched nontemporally.
-template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
+// short reductions keep the 128-row tile: the 256-row tile's per-tile ring fill and drain would
+// not amortise over fewer than 16 k-steps (at 16, GMM2 of DeepSeek-V3's shapes: the M = 65536 fp8 GMM2
+// 1.71 vs 1.57 PFLOPS, int8 1.97 vs 1.67 POPS, config 4's fp8 GMM2 116 vs 122 us)
+__host__ __device__ constexpr bool big_tall(int allow256, int K, int dt)
 {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
-    const int pos = xcd_position();
-    // short reductions keep the 128-row tile: the 256-row tile's per-tile ring fill and drain would
-    // not amortise over fewer than 16 k-steps (at 16, GMM2 of DeepSeek-V3's shapes: the M = 65536 fp8 GMM2
-    // 1.71 vs 1.57 PFLOPS, int8 1.97 vs 1.67 POPS, config 4's fp8 GMM2 116 vs 122 us)
-    const int nk = (int)((uint32_t)p.K * (DT == DT_BF16 ? 2 : 1) / GKB);
+    return allow256 && (int)((uint32_t)K * (dt == DT_BF16 ? 2 : 1) / GKB) >= CAM_GMM_MIN_NK256;
+}
+template <int DT> __device__ __forceinline__ ClassRanges big_ranges(bool tall)
+{
     constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
-    const bool tall = p.allow256 && nk >= CAM_GMM_MIN_NK256;
-    // every class's expert table, from one read of the counts
-    build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem),
-                                     tall ? ClassRanges{{G_HEAVY_ROWS, SMALL, 1}, {0x7fffffff, G_HEAVY_ROWS, SMALL}}
-                                          : ClassRanges{{0, 0, 0}, {0, 0x7fffffff, 0}});
+    return tall ? ClassRanges{{G_HEAVY_ROWS, SMALL, 1}, {0x7fffffff, G_HEAVY_ROWS, SMALL}}
+                : ClassRanges{{0, 0, 0}, {0, 0x7fffffff, 0}};
+}
+
+// The 8-wave schedule of one GEMM over the tile classes of the launch's tables (gmm_kernel_big).  ROLE !=
+// SYNC_NONE (the chained kernel): the 32-row class keeps the block's other four waves as spectators instead of
+// ending them, since the block has more work after it.
+template <int DT, int EPI, int ROLE>
+__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall, const GmmSync &sy)
+{
+    const int pos = xcd_position();
+    constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
+    constexpr bool KEEP = ROLE != SYNC_NONE;
     if (!tall) {
-        gmm_body<DT, EPI, 128>(p, gt, -1);
+        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1, sy);
         return;
     }
     // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
@@ -1147,8 +1347,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
         const int len = heavy_in(xcd);
         if (slot < len) {
-            gmm_body<DT, EPI, 256>(p, gt, 0x3fffffff, xcd * hx + slot,
-                                   (len - slot + S - 1) / S, S);
+            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, 0x3fffffff, xcd * hx + slot, (len - slot + S - 1) / S, S, sy);
             lds_sync();  // every wave is done with the first class's ring
         }
         int free_before = 0, free_all = 0;
@@ -1160,28 +1359,28 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
         const bool is_free = slot >= len;
         const int fpos = free_before + slot - len;  // the block's rank among the free blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true>(p, gt, run * free_all + (int)blockIdx.x,
-                                         is_free ? fpos * run : 0, is_free ? run : 0);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + (int)blockIdx.x, is_free ? fpos * run : 0,
+                                               is_free ? run : 0, 1, sy);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
-                if (threadIdx.x >= Tile<32>::THREADS)
+                if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
-                gmm_body<DT, EPI, 32, true>(p, gt, run32 * free_all + (int)blockIdx.x,
-                                            is_free ? fpos * run32 : 0, is_free ? run32 : 0);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + (int)blockIdx.x,
+                                                  is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1, sy);
             }
         }
         return;
     }
     if (n_heavy == 0) {  // one class after another, each balanced over the blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true>(p, gt, -1);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1, sy);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
-                if (threadIdx.x >= Tile<32>::THREADS)
+                if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;
-                gmm_body<DT, EPI, 32, true>(p, gt, -1);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1, sy);
             }
         }
         return;
@@ -1191,24 +1390,60 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     // light tiles with a run of about one heavy tile's worth each; the rest of the light tiles go
     // round-robin over all blocks (measured on config 4's GMM2, 364 heavy tiles on 256 blocks: the light
     // tiles' round-robin then no longer lands on blocks still busy with their second heavy tile).
-    gmm_body<DT, EPI, 256>(p, gt, pos);
+    gmm_body<DT, EPI, 256, false, ROLE>(p, gt, pos, 0, 0, 1, sy);
     lds_sync();  // every wave is done with the first class's ring
     const int r = heavy_tiles % G;
     const int nfree = r > 0 ? G - r : 0;
     const bool is_free = nfree > 0 && pos >= r;
     const int fpos = pos - r;
     if (has_mid)
-        gmm_body<DT, EPI, 128, true>(p, gt, run * nfree + pos, is_free ? fpos * run : 0,
-                                     is_free ? run : 0);
+        gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * nfree + pos, is_free ? fpos * run : 0, is_free ? run : 0, 1,
+                                           sy);
     if constexpr (SMALL > 1) {
         if (has_small) {
             lds_sync();
-            if (threadIdx.x >= Tile<32>::THREADS)
+            if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                 return;
-            gmm_body<DT, EPI, 32, true>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0,
-                                        is_free ? run32 : 0);
+            gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0,
+                                              is_free ? run32 : 0, 1, sy);
         }
     }
+}
+
+template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_big(GmmArgs p)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
+    const bool tall = big_tall(p.allow256, p.K, DT);
+    // every class's expert table, from one read of the counts
+    build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
+    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall, GmmSync{nullptr, 0, 0});
+}
+
+// Chained GMM1 + SwiGLU -> GMM2 (launch_gmm_chain): one table build, every block's GMM1 tiles (producing), then
+// its GMM2 tiles (consuming).  A block only ever waits for GMM1 tiles, and every block runs all of its GMM1
+// tiles before its first wait, so with every block resident each wait ends; a wait that outlasts the bound
+// gives up instead (and the host reads the sync status).  The grid is one block per CU, the blocks' LDS keeps
+// them to one per CU.
+template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_big(GmmArgs p1, GmmArgs p2, GmmSync sy)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
+    const bool tall = big_tall(p1.allow256, p1.K, DT);  // the host checked that GMM2 makes the same choice
+    build_group_tables<GMAX_THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
+    big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall, sy);
+    lds_sync();  // every wave is done with GMM1's last ring
+    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall, sy);
+}
+template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_small(GmmArgs p1, GmmArgs p2, GmmSync sy)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_SMALL_BYTES - sizeof(GroupTables));
+    build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
+                                          ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
+    gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE>(p1, gt, -1, 0, 0, 1, sy);
+    lds_sync();
+    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1, 0, 0, 1, sy);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
@@ -1301,6 +1536,92 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
             return launch_one<DT_FP8, EPI_SWIGLU_BF16>(a, s);
     }
     return hipErrorInvalidValue;
+}
+
+// ---- chained GMM1 -> GMM2
+#ifndef CAM_GMM_CHAIN_BIG
+#define CAM_GMM_CHAIN_BIG 0  // the prefill-sized chained kernel (8 waves, all tile classes)
+#endif
+int gmm_chain_counters(int M, int L) { return M / 32 + L + 1; }  // M-tiles of every class together, at most
+
+static bool chain_small(const GmmArgs &g) { return g.M <= 48 * g.L; }
+
+bool gmm_chain_supported(const GmmArgs &g1, const GmmArgs &g2, int dt)
+{
+    if (dt != DT_FP8 && dt != DT_BF16)
+        return false;  // int8 requantises h per token in a launch of its own
+    if (g1.M != g2.M || g1.L != g2.L || g1.group_list != g2.group_list || g2.K * 2 != g1.N)
+        return false;
+    if (chain_small(g1))
+        return true;
+#if !CAM_GMM_CHAIN_BIG
+    return false;
+#endif
+    const int allow = g1.M >= G_HEAVY_ROWS;
+    return big_tall(allow, g1.K, dt) == big_tall(allow, g2.K, dt);  // both GEMMs split every expert alike
+}
+
+static std::atomic<long long> g_sync_ticks{0};
+static std::atomic<int> g_sync_unreach{0};
+void sync_debug_set(long long wait_ticks, int unreachable)
+{
+    g_sync_ticks.store(wait_ticks, std::memory_order_relaxed);
+    g_sync_unreach.store(unreachable ? 1 : 0, std::memory_order_relaxed);
+}
+
+hipError_t sync_status_read(int *status, bool clear)
+{
+    int v = 0;
+    hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_cam_sync_status), sizeof(int), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess)
+        return e;
+    if (clear && v != 0) {
+        const int zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_cam_sync_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice);
+        if (e != hipSuccess)
+            return e;
+    }
+    *status = v;
+    return hipSuccess;
+}
+
+template <int DT, int EPI1> static hipError_t launch_chain_t(GmmArgs g1, GmmArgs g2, GmmSync sy, hipStream_t s)
+{
+    const int dev = current_device();
+    const int grid = (num_cus(dev) + 7) / 8 * 8;
+    if (chain_small(g1)) {
+        static std::atomic<bool> done[G_MAX_DEVICES];
+        hipError_t e = set_lds(gmm_chain_small<DT, EPI1>, G_LDS_SMALL_BYTES, dev, done);
+        if (e != hipSuccess)
+            return e;
+        hipLaunchKernelGGL((gmm_chain_small<DT, EPI1>), dim3(grid), dim3(256), G_LDS_SMALL_BYTES, s, g1, g2, sy);
+        return hipGetLastError();
+    }
+#if CAM_GMM_CHAIN_BIG
+    g1.allow256 = g2.allow256 = g1.M >= G_HEAVY_ROWS;
+    static std::atomic<bool> done[G_MAX_DEVICES];
+    hipError_t e = set_lds(gmm_chain_big<DT, EPI1>, G_LDS_BIG_BYTES, dev, done);
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL((gmm_chain_big<DT, EPI1>), dim3(grid), dim3(512), G_LDS_BIG_BYTES, s, g1, g2, sy);
+    return hipGetLastError();
+#else
+    return hipErrorNotSupported;
+#endif
+}
+
+hipError_t launch_gmm_chain(const GmmArgs &g1, const GmmArgs &g2, int dt, int *ready, hipStream_t s)
+{
+    if (g1.L <= 0 || g1.L > G_MAX_L || g1.M <= 0 || ready == nullptr)
+        return hipErrorInvalidValue;
+    if (!gmm_chain_supported(g1, g2, dt))
+        return hipErrorNotSupported;
+    const long long t = g_sync_ticks.load(std::memory_order_relaxed);
+    const GmmSync sy{ready, g1.N / 2 / 128 + g_sync_unreach.load(std::memory_order_relaxed),
+                     t > 0 ? t : 200000000LL};  // 2 s of the 100 MHz constant clock
+    if (dt == DT_FP8)
+        return launch_chain_t<DT_FP8, EPI_SWIGLU_FP8>(g1, g2, sy, s);
+    return launch_chain_t<DT_BF16, EPI_SWIGLU_BF16>(g1, g2, sy, s);
 }
 
 #ifdef CAM_GMM_TIMELINE

@@ -41,10 +41,12 @@ hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pre
 hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
                              int32_t *send_token_idx, void *ws, hipStream_t s);
 
-// decode-sized layout + count exchange in one launch (T*K <= 8192; ids masked by `active`)
+// decode-sized layout + count exchange in one launch (T*K <= 8192; ids masked by `active`); it also zeroes
+// zero[0, nzero) (a later launch's counters)
 hipError_t launch_layout_small(const int32_t *ids, const uint8_t *active, int T, int K, int E, int32_t *ids_eff,
                                int32_t *counts, int32_t *sti, int32_t *send_offset, int32_t *recv_count,
-                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s);
+                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s, int32_t *zero = nullptr,
+                               int nzero = 0);
 
 // ---- small utilities (notify.hip)
 hipError_t launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t s);

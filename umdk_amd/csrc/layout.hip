@@ -325,8 +325,10 @@ __global__ __launch_bounds__(SMALL_THREADS) void layout_small_kernel(
     const int32_t *__restrict__ ids, const uint8_t *__restrict__ active, int T, int K, int E,
     int32_t *__restrict__ ids_eff, int32_t *__restrict__ counts, int32_t *__restrict__ sti,
     int32_t *__restrict__ send_offset, int32_t *__restrict__ recv_count, int32_t *__restrict__ total,
-    int64_t *__restrict__ tokens_per_expert)
+    int64_t *__restrict__ tokens_per_expert, int32_t *__restrict__ zero, int nzero)
 {
+    for (int i = threadIdx.x; i < nzero; i += SMALL_THREADS)
+        zero[i] = 0;
     __shared__ int32_t run[MAX_E];
     __shared__ int32_t wave_hist[SMALL_WAVES][MAX_E];
     __shared__ int32_t wsum[SMALL_WAVES];
@@ -406,12 +408,13 @@ __global__ __launch_bounds__(SMALL_THREADS) void layout_small_kernel(
 
 hipError_t launch_layout_small(const int32_t *ids, const uint8_t *active, int T, int K, int E, int32_t *ids_eff,
                                int32_t *counts, int32_t *sti, int32_t *send_offset, int32_t *recv_count,
-                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s)
+                               int32_t *total, int64_t *tokens_per_expert, hipStream_t s, int32_t *zero,
+                               int nzero)
 {
-    if (T * K > 8192 || E > MAX_E || E > SMALL_THREADS)
+    if (T * K > 8192 || E > MAX_E || E > SMALL_THREADS || nzero < 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(layout_small_kernel, dim3(1), dim3(SMALL_THREADS), 0, s, ids, active, T, K, E, ids_eff, counts,
-                       sti, send_offset, recv_count, total, tokens_per_expert);
+                       sti, send_offset, recv_count, total, tokens_per_expert, zero, nzero);
     return hipGetLastError();
 }
 

@@ -152,6 +152,13 @@ class MoeLayerPlan(MoePrefillPlan):
         ws1 = _lib.workspace_size("camhipGroupedMatmulSwiglu", 1, 1, 1, L, N, H, 2 * I, 1, 1, self._dt(), 0,
                                   self._out_quant(), 1, 1)
         self.ws_gmm1 = torch.empty(max(ws1, 1), dtype=torch.uint8, device=dev) if ws1 else None
+        # both GEMMs in one call (camhipMoeExperts: one chained launch where the kernel exists); int8 keeps
+        # the two calls (its h is requantised per token in a launch of its own)
+        self.ws_experts = None
+        if dtype != "int8":
+            wsx = _lib.workspace_size("camhipMoeExperts", 1, 1, 1, L, N, H, 2 * I, 1, 1, 1, 1, self._dt(), 1, 1, 1,
+                                      1)
+            self.ws_experts = torch.empty(max(wsx, 1), dtype=torch.uint8, device=dev)
         self.topk_idx = torch.empty((T, K), dtype=torch.int32, device=dev)
 
     def route(self, logits, bias=None, stream=None):
@@ -160,8 +167,17 @@ class MoeLayerPlan(MoePrefillPlan):
                     self.topk_idx64.data_ptr(), stream=stream, device=self.device)
 
     def experts(self, w1, w1_scale, w2, w2_scale, stream=None):
-        self.gmm1(w1, w1_scale, stream)
-        return self.gmm2(w2, w2_scale, stream)
+        """GMM1 + SwiGLU and GMM2 over the dispatched rows -> self.y (bit-identical to gmm1() then gmm2())."""
+        if self.ws_experts is None:
+            self.gmm1(w1, w1_scale, stream)
+            return self.gmm2(w2, w2_scale, stream)
+        dt = self._dt()
+        p = lambda t: None if t is None else t.data_ptr()
+        _lib.launch("camhipMoeExperts", self.expand_x.data_ptr(), self.scales.data_ptr() if dt else None,
+                    self.recv_tokens_per_expert.data_ptr(), self.L, self.N, self.H, 2 * self.I, w1.data_ptr(),
+                    p(w1_scale), w2.data_ptr(), p(w2_scale), dt, 1, self.h.data_ptr(), p(self.h_scale),
+                    self.y.data_ptr(), workspace=self.ws_experts, stream=stream, device=self.device)
+        return self.y
 
     def _dt(self):
         return {"bf16": 0, "int8": 2, "fp8": 3}[self.dtype]
