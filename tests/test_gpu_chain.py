@@ -125,6 +125,16 @@ CASES = [
     # every group at the 48-row average limit of the chained kernel, several tiles per group
     ([48] * 16, 2048, 1024, DT_FP8),
     ([45, 0, 48, 31, 47, 12, 48, 48], 2048, 1024, DT_BF16),
+    # prefill-sized groups (the 8-wave chained kernel): config 4's skew -- four heavy experts on 256-row tiles,
+    # light ones on 32-row tiles run by four of the eight waves
+    ([1226, 725, 643, 482] + [62, 46, 30, 21, 17, 9, 7, 5, 4, 3, 2, 2, 1, 1, 1, 1] + [0] * 12, 7168, 2048, DT_FP8),
+    # all three classes (256-, 128- and 32-row tiles) in both GEMMs
+    ([400, 100, 30, 0, 1000, 64, 63, 5], 2048, 2048, DT_FP8),
+    ([400, 100, 30, 0, 900, 64, 63, 5], 1024, 1024, DT_BF16),
+    # short reductions: the 128-row class only
+    ([100, 300, 5, 0, 700, 64, 63], 1024, 512, DT_FP8),
+    # GEMMs that would split the experts differently (GMM1 256-row tiles, GMM2 128-row): the two calls
+    ([400, 100, 30, 0, 1000, 64, 63, 5], 2048, 1024, DT_FP8),
 ]
 
 
@@ -167,11 +177,12 @@ def test_chain_graph_replays(lib):
     assert lib.sync_status() == 0
 
 
-def test_chain_wait_gives_up_when_unreachable(lib):
+@pytest.mark.parametrize("counts,H,I", [([3, 40, 0, 7, 25], 1024, 256), ([400, 100, 30, 0, 1000, 64, 63, 5], 2048, 2048)])
+def test_chain_wait_gives_up_when_unreachable(lib, counts, H, I):
     """Host-forced give-up: with every readiness target unreachable and a 20 us bound, each wait gives up,
     the launch ends normally and the sync status is set; a normal call afterwards is exact again."""
-    print("chain forced give-up: ragged fp8", flush=True)
-    c = Case([3, 40, 0, 7, 25], 1024, 256, DT_FP8, seed=5)
+    print(f"chain forced give-up: fp8 M={sum(counts)} H={H} I={I}", flush=True)
+    c = Case(counts, H, I, DT_FP8, seed=5)
     c.run_pair(lib)
     torch.cuda.synchronize()
     lib.sync_status(clear=True)

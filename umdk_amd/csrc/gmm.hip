@@ -127,6 +127,22 @@ struct GmmSync {
 // nonzero once a readiness wait has given up (sticky; read and cleared by the host, sync_status_read)
 __device__ int g_cam_sync_status;
 
+// The one argument of a chained kernel.  The GEMM loops already hold every scalar register they have, so the
+// chained kernels keep nothing of it resident: each use re-reads the field from the kernel-argument segment
+// through a pointer the compiler cannot see through (a scalar load), and each phase loads its own GEMM's
+// arguments when it starts.
+struct ChainParams {
+    GmmArgs g1, g2;
+    GmmSync sy;
+};
+__device__ __forceinline__ const ChainParams *chain_params()
+{
+    uint64_t a = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(a));
+    // (a constant-address-space origin: the loads stay scalar loads)
+    return (const ChainParams *)(const __attribute__((address_space(4))) ChainParams *)a;
+}
+
 // h stores of a producing GMM1 tile: agent-coherent (sc1, written through to memory), so that a GMM2 tile on
 // another XCD, whose L2 has never held these lines during the launch, reads them from memory
 // (global address-space pointers: the atomics then need no aperture check of a flat address)
@@ -330,7 +346,7 @@ __device__ __forceinline__ void lds_sync()
 // and only meet the block's barriers.
 template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM), int ROLE = SYNC_NONE>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gtab, int first, int rs = 0, int rn = 0,
-                                         int rstride = 1, const GmmSync &sy = GmmSync{nullptr, 0, 0})
+                                         int rstride = 1)
 {
     using TC = Tile<BM, small_bn(BM, EPI)>;
     constexpr int TBN = TC::BN;
@@ -350,14 +366,15 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     const int wm = w / TC::WAVES_N, wn = w % TC::WAVES_N;
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool PRODUCE = ROLE == SYNC_PRODUCE, CONSUME = ROLE == SYNC_CONSUME;
-    const bool spect = ROLE != SYNC_NONE && w >= NW;
-    // M-tiles of the classes before this one (the readiness counters' index base)
-    int cls_base = 0;
-    if constexpr (ROLE != SYNC_NONE) {
+    const bool spect = ROLE != SYNC_NONE && NW < 8 && w >= NW;  // (8-wave tiles never have spectators)
+    // M-tiles of the classes before this one (the readiness counters' index base), read when needed
+    auto cls_base = [&]() {
+        int b = 0;
 #pragma unroll
         for (int k = 0; k < tile_class(BM); ++k)
-            cls_base += gtab->tile_end[k][p.L - 1];
-    }
+            b += gtab->tile_end[k][p.L - 1];
+        return __builtin_amdgcn_readfirstlane(b);
+    };
     constexpr bool SWIGLU = EPI != EPI_PLAIN;
     constexpr bool FP8 = DT == DT_FP8;
     constexpr bool INT8 = DT == DT_INT8;
@@ -398,7 +415,6 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         uint32_t ga[A_LOADS], gb[B_LOADS], gs[TC::S_DMAS];
         int wsg, wsu;  // fp8: weight-scale row offsets (gate / up n-blocks, or the wave's column block)
         int active;    // some row of this wave lies inside the segment (an int: a bool tail makes struct copies go through scratch)
-        int mti;       // readiness counter of the tile's M-tile (chained launches)
     };
     auto setup = [&](int tile, Ctx &c) {
         int lo = 0, hi = p.L - 1;
@@ -427,8 +443,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         // a wave whose rows all lie past the segment skips its MFMAs (it still moves its share of the
         // DMA and meets every barrier): a tile of a short segment costs little more than its weights
         c.active = !spect && c.row0 + wm * WM < c.seg1;
-        if constexpr (ROLE != SYNC_NONE)
-            c.mti = cls_base + tile_prefix(e) + mt;
+
         if (p.Wl) {  // separated weights: one allocation per expert, pointers read by scalar loads (a vector
                      // load here would make the tile switch wait for every DMA in flight)
             c.wbase = reinterpret_cast<const uint8_t *>(
@@ -704,19 +719,24 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     // ---- readiness (chained launches).  A producer counts a tile once every wave's h stores have completed:
     // each wave's vmcnt wait that covers them, then a barrier, then one atomic add by thread 0.  A consumer
     // wave polls the counter of the tile's M-tile (lane 0, agent-coherent load) before the tile's first DMA.
+    auto SY = [&]() -> GmmSync { return chain_params()->sy; };  // (chained kernels only)
+    // the counter of a tile's M-tile, from its context
+    auto mti_ctx = [&](const Ctx &c) {
+        return cls_base() + tile_prefix(c.e) + (c.row0 - row_off(c.e)) / GBM;
+    };
     int sig = -1;      // producer: counter of the tile whose stores are still to be counted
     int gave_up = 0;   // consumer: a wait of this wave gave up (the launch's outputs are void; no more waits)
     auto signal = [&]() {
         if constexpr (PRODUCE) {
             if (sig >= 0 && threadIdx.x == 0)
-                __hip_atomic_fetch_add(gptr(sy.ready + sig), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(gptr(SY().ready + sig), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sig = -1;
         }
     };
     auto poll = [&](int m) -> int {
         int v = 0;
         if (lane == 0)
-            v = __hip_atomic_load(gptr(sy.ready + m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v = __hip_atomic_load(gptr(SY().ready + m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return __builtin_amdgcn_readfirstlane(v);
     };
     auto wait_ready = [&](int m) {
@@ -724,8 +744,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             if (spect || gave_up)
                 return;
             const uint64_t t0 = wall_clock64();
-            while (poll(m) < sy.target) {
-                if ((long long)(wall_clock64() - t0) > sy.ticks) {
+            while (poll(m) < SY().target) {
+                if ((long long)(wall_clock64() - t0) > SY().ticks) {
                     if (lane == 0)
                         __hip_atomic_fetch_or(gptr(&g_cam_sync_status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     gave_up = 1;
@@ -751,7 +771,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         const int mt_e = tile_end[e] - tile_prefix(e);
         const int grp = local / (GM * ntn), rem = local % (GM * ntn);
         const int gm = min(GM, mt_e - grp * GM);
-        return cls_base + tile_prefix(e) + grp * GM + rem % gm;
+        return cls_base() + tile_prefix(e) + grp * GM + rem % gm;
     };
 
     if constexpr (BM >= 256) {
@@ -766,7 +786,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         // and no block scaling (measured against the generic two-stage loop, which waits for the whole ring
         // at every k-step: config 3's bf16 GEMMs 1.16 -> 1.27 PFLOPS, the int8 M-sweep's GMM1 +11%).
         static_assert(GSTAGES == 2, "two-stage ring");
-        constexpr int AHEAD = 2;
+        // A rows read ahead of their MFMAs (1, 2 or 3 measured within 1% of each other); the chained kernel
+        // reads one row ahead, whose registers its scalar spill lanes need
+        constexpr int AHEAD = ROLE == SYNC_NONE ? 2 : 1;
         // a tile's first DMAs: the W bands of k-step 0, its A bands and scales, then the W bands of k-step 1
         auto prime = [&](const Ctx &c) {
 #pragma unroll
@@ -785,7 +807,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         CAM_TL_DECL
         if (tile < total) {
             setup(tile, c);
-            wait_ready(c.mti);
+            wait_ready(mti_ctx(c));
             prime(c);
         }
         int next_ready = 0;  // consumer: the next tile's counter, polled while this tile's ring drains
@@ -926,7 +948,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             dequant_int8(c);
             epilogue(c);
             if constexpr (PRODUCE)
-                sig = c.mti;
+                sig = mti_ctx(c);
             CAM_TL_REC(c.e, tile);
             // int8: the dequantisation's loads have landed before the next tile (otherwise the compiler,
             // unsure of them, waits for every DMA in flight inside the k-loop)
@@ -936,8 +958,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             if (tile < total) {
                 setup(tile, c);
                 if constexpr (CONSUME) {
-                    if (next_ready < sy.target)
-                        wait_ready(c.mti);
+                    if (next_ready < SY().target)
+                        wait_ready(mti_ctx(c));
                 }
                 prime(c);
             }
@@ -966,11 +988,20 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         int kb = 0;          // the block's k-steps before the current tile
         bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
         int cur_ready = 0;    // consumer: the current tile's counter as polled before the previous tile's epilogue
-        // A consumer chains into its next tile only when that tile's rows are ready: wave 0 copies the
-        // counter into LDS by DMA at the tile's start, every wave reads it at k-step edge STAGES-2 (the copy
-        // has landed by then, as the producer's stores have), which precedes the first past-the-end DMA.
-        constexpr int SYNC_EDGE = GSTAGES - 2;
-        const bool can_chain = nk >= GSTAGES && (!CONSUME || nk >= SYNC_EDGE + GSTAGES);
+        const bool can_chain = nk >= GSTAGES;
+        // A consumer chains into its next tile only when that tile's rows are ready.  Nothing of this runs
+        // inside the k-loop (a branch there makes the compiler duplicate the loop): wave 0 copies the counter
+        // of the tile after next into an LDS slot by DMA at each tile's start, and every wave reads the next
+        // tile's slot after the tile's first barrier -- the copy was issued a whole tile earlier, and that
+        // tile's k-step waits have covered it.  The block's second tile's counter is copied before its first
+        // tile's DMAs.  Two slots of 64 ints (a DMA writes one per lane) in the exchange area, which the plain
+        // epilogue does not use; tile k's counter goes to slot k & 1.
+        int *rslot = scratch;
+        if constexpr (CONSUME) {
+            const int t1 = seq(1);
+            if (t1 < total && w == 0)
+                dma4_sc1(SY().ready + mti_of(t1), rslot + 64);
+        }
         while (true) {
             const int ntile = seq(++kt);
             const bool has_next = ntile < total;
@@ -981,7 +1012,6 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 setup(ntile, nxt);
             else
                 nxt = cur;
-            bool poll_next = false;  // consumer: the next tile's counter is on its way into LDS
             auto slot = [&](int ks) { return (kb + ks) % GSTAGES; };
             auto stage_ptr = [&](int ks) { return smem + slot(ks) * STAGE_BYTES; };
             // DMA instruction q of the current tile's k-step ksx (ksx may run past the end)
@@ -1003,22 +1033,14 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             };
             if (!primed) {
                 if constexpr (CONSUME) {
-                    if (cur_ready < sy.target)
-                        wait_ready(cur.mti);
+                    if (cur_ready < SY().target)
+                        wait_ready(mti_ctx(cur));
                 }
 #pragma unroll
                 for (int s0 = 0; s0 < GSTAGES; ++s0)
 #pragma unroll
                     for (int q = 0; q < LOADS; ++q)
                         dma_one(cur, min(s0, nk - 1), slot(s0), q);
-            }
-            if constexpr (CONSUME) {
-                if (chain) {
-                    chain = 0;
-                    poll_next = true;
-                    if (w == 0)
-                        dma4_sc1(sy.ready + nxt.mti, scratch);
-                }
             }
             wait_vmcnt<LOADS *(GSTAGES - 1)>();  // k-step 0 has landed
             bar();
@@ -1027,26 +1049,20 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 if (!primed)
                     signal();
             }
+            if constexpr (CONSUME) {
+                // the next tile's counter (bar() is a compiler memory barrier: the slot is read afresh), then
+                // the copy of the one after it into the slot this tile's counter occupied
+                if (chain)
+                    chain = rslot[(kt & 1) * 64] >= SY().target;
+                const int t2 = seq(kt + 1);
+                if (t2 < total && w == 0)
+                    dma4_sc1(SY().ready + mti_of(t2), rslot + ((kt + 1) & 1) * 64);
+            }
             clear_acc();
             // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
-            int edge = 0;
             auto step_edge = [&]() {
                 wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
                 bar();
-                if constexpr (ROLE != SYNC_NONE) {
-                    // edge SYNC_EDGE: every op a wave issued before this tile's k-loop has completed (only
-                    // LOADS (STAGES - 2) may be in flight, all issued since): the previous tile's h stores
-                    // (producer, chained tile) and wave 0's copy of the next tile's counter (consumer)
-                    if (edge == SYNC_EDGE) {
-                        if constexpr (PRODUCE)
-                            signal();
-                        if constexpr (CONSUME) {
-                            if (poll_next)
-                                chain = scratch[0] >= sy.target;  // (bar() is a compiler memory barrier: read afresh)
-                        }
-                    }
-                    ++edge;
-                }
             };
 
             if constexpr (FP8) {
@@ -1209,18 +1225,21 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                     kloop(std::false_type{});
             }
 
+            // producer, primed tile: the previous tile's stores are counted now -- the k-loop's last edge left
+            // at most LOADS (STAGES - 2) DMAs in flight in every wave, all issued after those stores
+            signal();
             dequant_int8(cur);
             if (!chain) {
                 if constexpr (CONSUME) {
                     if (has_next && !gave_up && !spect)
-                        cur_ready = poll(nxt.mti);  // answered while the ring drains
+                        cur_ready = poll(mti_ctx(nxt));  // answered while the ring drains
                 }
                 wait_vmcnt<0>();  // the tail's reloads have landed before the next tile reuses the ring
                 bar();
             }
             epilogue(cur);
             if constexpr (PRODUCE)
-                sig = cur.mti;
+                sig = mti_ctx(cur);
             CAM_TL_REC(cur.e, tile);
             kb += nk;
             if (!has_next)
@@ -1317,13 +1336,13 @@ template <int DT> __device__ __forceinline__ ClassRanges big_ranges(bool tall)
 // SYNC_NONE (the chained kernel): the 32-row class keeps the block's other four waves as spectators instead of
 // ending them, since the block has more work after it.
 template <int DT, int EPI, int ROLE>
-__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall, const GmmSync &sy)
+__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall)
 {
     const int pos = xcd_position();
     constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
     constexpr bool KEEP = ROLE != SYNC_NONE;
     if (!tall) {
-        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1, sy);
+        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1);
         return;
     }
     // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
@@ -1347,7 +1366,7 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
         const int len = heavy_in(xcd);
         if (slot < len) {
-            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, 0x3fffffff, xcd * hx + slot, (len - slot + S - 1) / S, S, sy);
+            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, 0x3fffffff, xcd * hx + slot, (len - slot + S - 1) / S, S);
             lds_sync();  // every wave is done with the first class's ring
         }
         int free_before = 0, free_all = 0;
@@ -1360,27 +1379,27 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         const int fpos = free_before + slot - len;  // the block's rank among the free blocks
         if (has_mid)
             gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + (int)blockIdx.x, is_free ? fpos * run : 0,
-                                               is_free ? run : 0, 1, sy);
+                                               is_free ? run : 0, 1);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
                 if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
                 gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + (int)blockIdx.x,
-                                                  is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1, sy);
+                                                  is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1);
             }
         }
         return;
     }
     if (n_heavy == 0) {  // one class after another, each balanced over the blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1, sy);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
                 if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1, sy);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1);
             }
         }
         return;
@@ -1390,22 +1409,21 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
     // light tiles with a run of about one heavy tile's worth each; the rest of the light tiles go
     // round-robin over all blocks (measured on config 4's GMM2, 364 heavy tiles on 256 blocks: the light
     // tiles' round-robin then no longer lands on blocks still busy with their second heavy tile).
-    gmm_body<DT, EPI, 256, false, ROLE>(p, gt, pos, 0, 0, 1, sy);
+    gmm_body<DT, EPI, 256, false, ROLE>(p, gt, pos, 0, 0, 1);
     lds_sync();  // every wave is done with the first class's ring
     const int r = heavy_tiles % G;
     const int nfree = r > 0 ? G - r : 0;
     const bool is_free = nfree > 0 && pos >= r;
     const int fpos = pos - r;
     if (has_mid)
-        gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * nfree + pos, is_free ? fpos * run : 0, is_free ? run : 0, 1,
-                                           sy);
+        gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * nfree + pos, is_free ? fpos * run : 0, is_free ? run : 0, 1);
     if constexpr (SMALL > 1) {
         if (has_small) {
             lds_sync();
             if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                 return;
             gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0,
-                                              is_free ? run32 : 0, 1, sy);
+                                              is_free ? run32 : 0, 1);
         }
     }
 }
@@ -1417,7 +1435,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     const bool tall = big_tall(p.allow256, p.K, DT);
     // every class's expert table, from one read of the counts
     build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
-    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall, GmmSync{nullptr, 0, 0});
+    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall);
 }
 
 // Chained GMM1 + SwiGLU -> GMM2 (launch_gmm_chain): one table build, every block's GMM1 tiles (producing), then
@@ -1425,25 +1443,37 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
 // tiles before its first wait, so with every block resident each wait ends; a wait that outlasts the bound
 // gives up instead (and the host reads the sync status).  The grid is one block per CU, the blocks' LDS keeps
 // them to one per CU.
-template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_big(GmmArgs p1, GmmArgs p2, GmmSync sy)
+template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_big(ChainParams cp)
 {
+    (void)cp;  // read through chain_params()
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
-    const bool tall = big_tall(p1.allow256, p1.K, DT);  // the host checked that GMM2 makes the same choice
-    build_group_tables<GMAX_THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
-    big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall, sy);
+    bool tall;
+    {
+        const GmmArgs p1 = chain_params()->g1;
+        tall = big_tall(p1.allow256, p1.K, DT);  // the host checked that GMM2 makes the same choice
+        build_group_tables<GMAX_THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
+                                         big_ranges<DT>(tall));
+        big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall);
+    }
     lds_sync();  // every wave is done with GMM1's last ring
-    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall, sy);
+    const GmmArgs p2 = chain_params()->g2;
+    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall);
 }
-template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_small(GmmArgs p1, GmmArgs p2, GmmSync sy)
+template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_small(ChainParams cp)
 {
+    (void)cp;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_SMALL_BYTES - sizeof(GroupTables));
-    build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
-                                          ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
-    gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE>(p1, gt, -1, 0, 0, 1, sy);
+    {
+        const GmmArgs p1 = chain_params()->g1;
+        build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
+                                              ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
+        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE>(p1, gt, -1);
+    }
     lds_sync();
-    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1, 0, 0, 1, sy);
+    const GmmArgs p2 = chain_params()->g2;
+    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
@@ -1540,7 +1570,7 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
 
 // ---- chained GMM1 -> GMM2
 #ifndef CAM_GMM_CHAIN_BIG
-#define CAM_GMM_CHAIN_BIG 0  // the prefill-sized chained kernel (8 waves, all tile classes)
+#define CAM_GMM_CHAIN_BIG 1  // the prefill-sized chained kernel (8 waves, all tile classes)
 #endif
 int gmm_chain_counters(int M, int L) { return M / 32 + L + 1; }  // M-tiles of every class together, at most
 
@@ -1594,7 +1624,7 @@ template <int DT, int EPI1> static hipError_t launch_chain_t(GmmArgs g1, GmmArgs
         hipError_t e = set_lds(gmm_chain_small<DT, EPI1>, G_LDS_SMALL_BYTES, dev, done);
         if (e != hipSuccess)
             return e;
-        hipLaunchKernelGGL((gmm_chain_small<DT, EPI1>), dim3(grid), dim3(256), G_LDS_SMALL_BYTES, s, g1, g2, sy);
+        hipLaunchKernelGGL((gmm_chain_small<DT, EPI1>), dim3(grid), dim3(256), G_LDS_SMALL_BYTES, s, ChainParams{g1, g2, sy});
         return hipGetLastError();
     }
 #if CAM_GMM_CHAIN_BIG
@@ -1603,7 +1633,7 @@ template <int DT, int EPI1> static hipError_t launch_chain_t(GmmArgs g1, GmmArgs
     hipError_t e = set_lds(gmm_chain_big<DT, EPI1>, G_LDS_BIG_BYTES, dev, done);
     if (e != hipSuccess)
         return e;
-    hipLaunchKernelGGL((gmm_chain_big<DT, EPI1>), dim3(grid), dim3(512), G_LDS_BIG_BYTES, s, g1, g2, sy);
+    hipLaunchKernelGGL((gmm_chain_big<DT, EPI1>), dim3(grid), dim3(512), G_LDS_BIG_BYTES, s, ChainParams{g1, g2, sy});
     return hipGetLastError();
 #else
     return hipErrorNotSupported;
