@@ -150,11 +150,12 @@ def test_chain_matches_two_calls(lib, counts, H, I, dt):
     assert lib.sync_status() == 0
 
 
-def test_chain_graph_replays(lib):
+@pytest.mark.parametrize("counts", [decode_counts(seed=3), [1100, 700, 500, 3, 40, 0, 17, 9]])
+def test_chain_graph_replays(lib, counts):
     """The chained call captured in a HIP graph: every replay, with eager work and a reset of the outputs
     between replays, equals the two-call path."""
-    print("chain graph replays: config-5 shapes fp8", flush=True)
-    c = Case(decode_counts(seed=3), 7168, 2048, DT_FP8, seed=11)
+    print(f"chain graph replays: fp8 H=7168 I=2048 M={sum(counts)}", flush=True)
+    c = Case(counts, 7168, 2048, DT_FP8, seed=11)
     c.run_pair(lib)
     ws = torch.empty(lib.workspace_size("camhipMoeExperts", *c.chain_args()), dtype=torch.uint8, device="cuda")
     side = torch.cuda.Stream()
