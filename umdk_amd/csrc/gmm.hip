@@ -344,9 +344,12 @@ __device__ __forceinline__ void lds_sync()
 // sy.ready; SYNC_CONSUME tiles start their DMAs only once sy.ready of their M-tile has reached sy.target.  Waves
 // beyond the tile's own (a 32-row class run by an 8-wave block) are spectators: they issue no DMA, MFMA or store
 // and only meet the block's barriers.
-template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM), int ROLE = SYNC_NONE>
+// EAGER (the 4-wave chained kernel): a producer's primed tile counts its predecessor at k-step edge STAGES-2
+// instead of after its k-loop (a branch inside the k-loop, which the 8-wave kernels cannot afford).  bid: the
+// block's position for balanced placement (a chained consumer passes its arrival order), -1: blockIdx.x.
+template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM), int ROLE = SYNC_NONE, bool EAGER = false>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gtab, int first, int rs = 0, int rn = 0,
-                                         int rstride = 1)
+                                         int rstride = 1, int bid = -1)
 {
     using TC = Tile<BM, small_bn(BM, EPI)>;
     constexpr int TBN = TC::BN;
@@ -392,12 +395,13 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     // streaming a final partial round alone.  Otherwise the caller's position and the full grid stride.
     int G = gridDim.x, logical = first;
     if (first < 0) {
+        const int b = bid >= 0 ? bid : (int)blockIdx.x;
         const int rounds = max((total + G - 1) / G, 1);
         const int g_eff = min(G, ((total + rounds - 1) / rounds + 7) / 8 * 8);
-        if ((int)blockIdx.x >= g_eff)
+        if (b >= g_eff)
             return;
         G = g_eff;
-        logical = (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3));
+        logical = (b & 7) * (G >> 3) + (b >> 3);
     }
     // the block's k-th tile: the run, then the strided sequence
     auto seq = [&](int k) { return k < rn ? rs + k * rstride : logical + (k - rn) * G; };
@@ -1060,9 +1064,17 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             }
             clear_acc();
             // end of a k-step: k-step ks+1 has landed for every wave and every wave has read k-step ks
+            int edge = 0;
             auto step_edge = [&]() {
                 wait_vmcnt_lgkm0<LOADS *(GSTAGES - 2)>();
                 bar();
+                if constexpr (PRODUCE && EAGER) {
+                    // edge STAGES-2: only LOADS (STAGES - 2) DMAs, all issued during this k-loop, may still be in
+                    // flight in any wave, so the previous tile's h stores (issued before) have completed
+                    if (edge == GSTAGES - 2)
+                        signal();
+                    ++edge;
+                }
             };
 
             if constexpr (FP8) {
@@ -1335,14 +1347,16 @@ template <int DT> __device__ __forceinline__ ClassRanges big_ranges(bool tall)
 // The 8-wave schedule of one GEMM over the tile classes of the launch's tables (gmm_kernel_big).  ROLE !=
 // SYNC_NONE (the chained kernel): the 32-row class keeps the block's other four waves as spectators instead of
 // ending them, since the block has more work after it.
+// bid: the block's id for the placement (blockIdx.x; a chained consumer passes its arrival order, so that the
+// blocks that finish GMM1 first take the positions with the most GMM2 work).
 template <int DT, int EPI, int ROLE>
-__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall)
+__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall, int bid)
 {
-    const int pos = xcd_position();
+    const int pos = (gridDim.x & 7) ? bid : (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);  // XCD-aware order
     constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
     constexpr bool KEEP = ROLE != SYNC_NONE;
     if (!tall) {
-        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1);
+        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1, bid);
         return;
     }
     // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
@@ -1361,7 +1375,7 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         // The free blocks start on the light tiles at once, `run` (or `run32`) in a row each; the rest of
         // the light tiles go round-robin over all blocks in launch order (every XCD in turn), reaching the
         // heavy blocks as they finish.
-        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, S = G >> 3;
+        const int xcd = bid & 7, slot = bid >> 3, S = G >> 3;
         const int hx = (heavy_tiles + 7) / 8;
         auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
         const int len = heavy_in(xcd);
@@ -1378,14 +1392,14 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         const bool is_free = slot >= len;
         const int fpos = free_before + slot - len;  // the block's rank among the free blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + (int)blockIdx.x, is_free ? fpos * run : 0,
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + bid, is_free ? fpos * run : 0,
                                                is_free ? run : 0, 1);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
                 if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + (int)blockIdx.x,
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + bid,
                                                   is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1);
             }
         }
@@ -1393,13 +1407,13 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
     }
     if (n_heavy == 0) {  // one class after another, each balanced over the blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1, bid);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
                 if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
                     return;
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1, bid);
             }
         }
         return;
@@ -1435,7 +1449,7 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
     const bool tall = big_tall(p.allow256, p.K, DT);
     // every class's expert table, from one read of the counts
     build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
-    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall);
+    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall, (int)blockIdx.x);
 }
 
 // Chained GMM1 + SwiGLU -> GMM2 (launch_gmm_chain): one table build, every block's GMM1 tiles (producing), then
@@ -1443,6 +1457,23 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
 // tiles before its first wait, so with every block resident each wait ends; a wait that outlasts the bound
 // gives up instead (and the host reads the sync status).  The grid is one block per CU, the blocks' LDS keeps
 // them to one per CU.
+// The block's arrival order at the GMM1 -> GMM2 boundary, as a block id: its rank among the blocks of its XCD
+// (one counter per XCD, after the M-tile counters) in place of blockIdx.x >> 3.  The consumer phase places its
+// tiles by it: the blocks that finish GMM1 first take the positions that hold the most GMM2 work.
+__device__ __forceinline__ int arrival_bid(int M, int L, uint8_t *smem)
+{
+    int *slot = reinterpret_cast<int *>(smem);  // the ring is idle between the phases
+    const int xcd = blockIdx.x & 7;
+    if (threadIdx.x == 0) {
+        int *ctr = chain_params()->sy.ready + (M / 32 + L + 1) + xcd;
+        *slot = __hip_atomic_fetch_add(gptr(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const int r = *slot;
+    __syncthreads();  // (the slot is ring memory again)
+    return (gridDim.x & 7) ? (int)blockIdx.x : r * 8 + xcd;
+}
+
 template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_big(ChainParams cp)
 {
     (void)cp;  // read through chain_params()
@@ -1454,11 +1485,12 @@ template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_
         tall = big_tall(p1.allow256, p1.K, DT);  // the host checked that GMM2 makes the same choice
         build_group_tables<GMAX_THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
                                          big_ranges<DT>(tall));
-        big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall);
+        big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall, (int)blockIdx.x);
     }
     lds_sync();  // every wave is done with GMM1's last ring
     const GmmArgs p2 = chain_params()->g2;
-    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall);
+    const int bid = arrival_bid(p2.M, p2.L, smem);
+    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall, bid);
 }
 template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_small(ChainParams cp)
 {
@@ -1469,11 +1501,12 @@ template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_
         const GmmArgs p1 = chain_params()->g1;
         build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
                                               ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
-        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE>(p1, gt, -1);
+        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE, true>(p1, gt, -1);
     }
     lds_sync();
     const GmmArgs p2 = chain_params()->g2;
-    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1);
+    const int bid = arrival_bid(p2.M, p2.L, smem);
+    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1, 0, 0, 1, bid);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
@@ -1572,7 +1605,8 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
 #ifndef CAM_GMM_CHAIN_BIG
 #define CAM_GMM_CHAIN_BIG 1  // the prefill-sized chained kernel (8 waves, all tile classes)
 #endif
-int gmm_chain_counters(int M, int L) { return M / 32 + L + 1; }  // M-tiles of every class together, at most
+// the M-tiles of every class together (at most M/32 + L), then one arrival counter per XCD
+int gmm_chain_counters(int M, int L) { return M / 32 + L + 1 + 8; }
 
 static bool chain_small(const GmmArgs &g) { return g.M <= 48 * g.L; }
 
