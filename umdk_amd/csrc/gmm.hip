@@ -43,6 +43,7 @@
 //     blocks of one XCD take consecutive tiles: they share A and W tiles in
 //     that XCD's L2.
 #include <algorithm>
+#include <cstdlib>
 #include <atomic>
 #include <type_traits>
 
@@ -142,6 +143,11 @@ __device__ __forceinline__ const ChainParams *chain_params()
     // (a constant-address-space origin: the loads stay scalar loads)
     return (const ChainParams *)(const __attribute__((address_space(4))) ChainParams *)a;
 }
+
+// readiness counters of a chained launch: the M-tiles (at most M/32 + L), then one arrival counter per XCD,
+// then one heavy-tile queue per XCD
+__host__ __device__ constexpr int chain_arrival_index(int M, int L) { return M / 32 + L + 1; }
+__host__ __device__ constexpr int chain_queue_index(int M, int L) { return chain_arrival_index(M, L) + 8; }
 
 // h stores of a producing GMM1 tile: agent-coherent (sc1, written through to memory), so that a GMM2 tile on
 // another XCD, whose L2 has never held these lines during the launch, reads them from memory
@@ -338,12 +344,14 @@ __device__ __forceinline__ void lds_sync()
 }
 
 // Tiles of the experts with a row count in [lo, hi); this block takes tiles first, first + G, ...
-// (first < 0: balanced placement, see below), preceded by a run of rn tiles rs, rs + rstride, ... (an
+// (first == -1: balanced placement, see below; G_DYN: a dynamic queue), preceded by a run of rn tiles rs, rs + rstride, ... (an
 // increasing sequence: the first index past the class's tiles ends it).
 // ROLE (chained launches only): SYNC_PRODUCE tiles store h agent-coherently and count each finished tile in
 // sy.ready; SYNC_CONSUME tiles start their DMAs only once sy.ready of their M-tile has reached sy.target.  Waves
 // beyond the tile's own (a 32-row class run by an 8-wave block) are spectators: they issue no DMA, MFMA or store
 // and only meet the block's barriers.
+constexpr int G_DYN = -2;  // gmm_body's `first` for a dynamic tile queue (see there)
+
 // EAGER (the 4-wave chained kernel): a producer's primed tile counts its predecessor at k-step edge STAGES-2
 // instead of after its k-loop (a branch inside the k-loop, which the 8-wave kernels cannot afford).  bid: the
 // block's position for balanced placement (a chained consumer passes its arrival order), -1: blockIdx.x.
@@ -389,12 +397,15 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     const int ntn = SWIGLU ? half_n / 128 : p.N / TBN;
     const int total = __builtin_amdgcn_readfirstlane(tile_prefix(p.L)) * ntn;
 
-    // first < 0: this launch has one tile class, so balance it: with R = ceil(total / grid) rounds, only
+    // first == -1: this launch has one tile class, so balance it: with R = ceil(total / grid) rounds, only
     // the first ceil(total / R) blocks (rounded up to whole XCDs) take tiles, R each at most.  A weight
     // stream is bound by aggregate HBM bandwidth, which that many CUs still saturate, and no CU is left
     // streaming a final partial round alone.  Otherwise the caller's position and the full grid stride.
     int G = gridDim.x, logical = first;
-    if (first < 0) {
+    // G_DYN (chained consumer, 256-row tiles): tiles rs, rs + 1, ... rs + rn - 1 handed out one at a time by
+    // the queue counter SY().ready[rstride], shared by the blocks of one XCD
+    const bool dyn = CONSUME && BM >= 256 && first == G_DYN;
+    if (first == -1) {
         const int b = bid >= 0 ? bid : (int)blockIdx.x;
         const int rounds = max((total + G - 1) / G, 1);
         const int g_eff = min(G, ((total + rounds - 1) / rounds + 7) / 8 * 8);
@@ -806,7 +817,29 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
                 dma_one(c, min(1, nk - 1), 1, q);
         };
-        int kt = 0, tile = seq(0);
+        // dynamic queue: thread 0 takes the next index and publishes the tile through the (plain-epilogue,
+        // so unused) exchange area; past the queue's end, `total`
+        int *qslot = reinterpret_cast<int *>(scratch) + 128;
+        auto take = [&]() {
+            if constexpr (CONSUME) {
+                return __hip_atomic_fetch_add(gptr(SY().ready + rstride), 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return 0;
+        };
+        auto publish = [&](int k) {
+            if (threadIdx.x == 0)
+                *qslot = k < rn ? rs + k : total;
+            lds_sync();
+            return __builtin_amdgcn_readfirstlane(*qslot);
+        };
+        int kt = 0, tile;
+        if (dyn) {
+            const int k = threadIdx.x == 0 ? take() : 0;
+            tile = publish(k);
+        } else {
+            tile = seq(0);
+        }
         Ctx c;
         CAM_TL_DECL
         if (tile < total) {
@@ -942,13 +975,24 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                     for (int q = 0; q < 4; ++q)
                         acc[IF - 1][j][q] += pend[j][q] * ps[j];
             }
-            if constexpr (CONSUME) {
-                const int ntile = seq(kt + 1);
-                if (ntile < total && !gave_up && !spect)
-                    next_ready = poll(mti_of(ntile));  // answered while the ring drains
+            int ntile = 0;
+            if (dyn) {
+                // the queue's answer arrives while the ring drains; then the next tile's counter, answered
+                // during the epilogue
+                const int k = threadIdx.x == 0 ? take() : 0;
+                wait_vmcnt<0>();
+                ntile = publish(k);
+                if (ntile < total && !gave_up)
+                    next_ready = poll(mti_of(ntile));
+            } else {
+                if constexpr (CONSUME) {
+                    ntile = seq(kt + 1);
+                    if (ntile < total && !gave_up && !spect)
+                        next_ready = poll(mti_of(ntile));  // answered while the ring drains
+                }
+                wait_vmcnt<0>();  // the tail's reload has landed before the next tile reuses the ring
+                bar();
             }
-            wait_vmcnt<0>();  // the tail's reload has landed before the next tile reuses the ring
-            bar();
             dequant_int8(c);
             epilogue(c);
             if constexpr (PRODUCE)
@@ -958,7 +1002,8 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             // unsure of them, waits for every DMA in flight inside the k-loop)
             if constexpr (INT8)
                 wait_vmcnt<0>();
-            tile = seq(++kt);
+            ++kt;
+            tile = dyn ? ntile : seq(kt);
             if (tile < total) {
                 setup(tile, c);
                 if constexpr (CONSUME) {
@@ -992,7 +1037,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         int kb = 0;          // the block's k-steps before the current tile
         bool primed = false;  // the current tile's first STAGES k-steps were issued by the previous tile
         int cur_ready = 0;    // consumer: the current tile's counter as polled before the previous tile's epilogue
-        const bool can_chain = nk >= GSTAGES;
+        const bool can_chain = nk >= GSTAGES && (!(CONSUME && EAGER) || nk >= 2 * GSTAGES - 2);
         // A consumer chains into its next tile only when that tile's rows are ready.  Nothing of this runs
         // inside the k-loop (a branch there makes the compiler duplicate the loop): wave 0 copies the counter
         // of the tile after next into an LDS slot by DMA at each tile's start, and every wave reads the next
@@ -1001,7 +1046,12 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         // tile's DMAs.  Two slots of 64 ints (a DMA writes one per lane) in the exchange area, which the plain
         // epilogue does not use; tile k's counter goes to slot k & 1.
         int *rslot = scratch;
-        if constexpr (CONSUME) {
+        // EAGER consumer (the 4-wave kernel, which affords a branch in its k-loop): the copy goes out at k-step
+        // edge nk - 2 STAGES + 2 and is read at edge nk - STAGES, just before the first past-the-end DMA, so the
+        // decision uses a counter value from late in the current tile
+        constexpr bool EAGER_C = CONSUME && EAGER;
+        const int e_copy = nk - 2 * GSTAGES + 2, e_read = nk - GSTAGES;
+        if constexpr (CONSUME && !EAGER) {
             const int t1 = seq(1);
             if (t1 < total && w == 0)
                 dma4_sc1(SY().ready + mti_of(t1), rslot + 64);
@@ -1053,7 +1103,10 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 if (!primed)
                     signal();
             }
-            if constexpr (CONSUME) {
+            const bool poll_next = chain;  // EAGER consumer: decided inside the k-loop
+            if constexpr (EAGER_C)
+                chain = 0;
+            if constexpr (CONSUME && !EAGER) {
                 // the next tile's counter (bar() is a compiler memory barrier: the slot is read afresh), then
                 // the copy of the one after it into the slot this tile's counter occupied
                 if (chain)
@@ -1073,8 +1126,18 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                     // flight in any wave, so the previous tile's h stores (issued before) have completed
                     if (edge == GSTAGES - 2)
                         signal();
-                    ++edge;
                 }
+                if constexpr (EAGER_C) {
+                    if (poll_next) {
+                        // the copy issued at e_copy has landed by e_read: STAGES - 2 k-steps of DMAs came after it
+                        if (edge == e_copy && w == 0)
+                            dma4_sc1(SY().ready + mti_ctx(nxt), scratch);
+                        if (edge == e_read)
+                            chain = scratch[0] >= SY().target;  // (bar() is a compiler memory barrier)
+                    }
+                }
+                if constexpr (EAGER)
+                    ++edge;
             };
 
             if constexpr (FP8) {
@@ -1369,6 +1432,27 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
     const int G = gridDim.x;
     // 256-row tiles: heavy M-tiles x N-tiles
     const int heavy_tiles = n_heavy * (EPI != EPI_PLAIN ? p.N / 2 / 128 : p.N / 256);
+    if constexpr (ROLE == SYNC_CONSUME) {
+        // Chained GMM2: the blocks reach it at different times (their GMM1 work differs), so the heavy tiles go
+        // out through dynamic queues, one per XCD over that XCD's consecutive share (tiles sharing its L2), to
+        // whichever of its blocks is free; the light tiles follow round-robin by the blocks' arrival order.
+        if (heavy_tiles > 0) {
+            const int nq = (G & 7) ? 1 : 8, x = nq == 1 ? 0 : (bid & 7);
+            const int hx = (heavy_tiles + nq - 1) / nq;
+            const int len = max(0, min(hx, heavy_tiles - x * hx));
+            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, G_DYN, x * hx, len, chain_queue_index(p.M, p.L) + x);
+            lds_sync();
+        }
+        if (has_mid)
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, pos, 0, 0, 1);
+        if constexpr (SMALL > 1) {
+            if (has_small) {
+                lds_sync();
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, pos, 0, 0, 1);
+            }
+        }
+        return;
+    }
     if (heavy_tiles > 0 && heavy_tiles < G && (G & 7) == 0) {
         // Fewer heavy tiles than blocks.  They are split evenly over the 8 XCDs (XCD x takes the run
         // [x hx, (x + 1) hx), consecutive tiles sharing that XCD's L2), so each XCD keeps some blocks free.
@@ -1465,7 +1549,7 @@ __device__ __forceinline__ int arrival_bid(int M, int L, uint8_t *smem)
     int *slot = reinterpret_cast<int *>(smem);  // the ring is idle between the phases
     const int xcd = blockIdx.x & 7;
     if (threadIdx.x == 0) {
-        int *ctr = chain_params()->sy.ready + (M / 32 + L + 1) + xcd;
+        int *ctr = chain_params()->sy.ready + chain_arrival_index(M, L) + xcd;
         *slot = __hip_atomic_fetch_add(gptr(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
@@ -1506,7 +1590,7 @@ template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_
     lds_sync();
     const GmmArgs p2 = chain_params()->g2;
     const int bid = arrival_bid(p2.M, p2.L, smem);
-    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME>(p2, gt, -1, 0, 0, 1, bid);
+    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME, true>(p2, gt, -1, 0, 0, 1, bid);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
@@ -1605,15 +1689,31 @@ hipError_t launch_gmm(const GmmArgs &a, int dt, int epi, hipStream_t s)
 #ifndef CAM_GMM_CHAIN_BIG
 #define CAM_GMM_CHAIN_BIG 1  // the prefill-sized chained kernel (8 waves, all tile classes)
 #endif
-// the M-tiles of every class together (at most M/32 + L), then one arrival counter per XCD
-int gmm_chain_counters(int M, int L) { return M / 32 + L + 1 + 8; }
+int gmm_chain_counters(int M, int L) { return chain_queue_index(M, L) + 8; }
 
 static bool chain_small(const GmmArgs &g) { return g.M <= 48 * g.L; }
+
+// CAMHIP_GMM_CHAIN=0 in the environment turns the chained launch off (the two-launch path runs instead; for
+// measuring one against the other)
+static bool chain_enabled()
+{
+    static const bool on = [] {
+        const char *v = getenv("CAMHIP_GMM_CHAIN");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+// h above this size is not chained: the producing tiles store it agent-coherently (written through to
+// memory), which for h of hundreds of MB (Mixtral-sized prefill) costs more than the overlap gains
+constexpr long long G_CHAIN_MAX_H_BYTES = 64ll << 20;
 
 bool gmm_chain_supported(const GmmArgs &g1, const GmmArgs &g2, int dt)
 {
     if (dt != DT_FP8 && dt != DT_BF16)
         return false;  // int8 requantises h per token in a launch of its own
+    if (!chain_enabled() || (long long)g1.M * (g1.N / 2) * (dt == DT_BF16 ? 2 : 1) > G_CHAIN_MAX_H_BYTES)
+        return false;
     if (g1.M != g2.M || g1.L != g2.L || g1.group_list != g2.group_list || g2.K * 2 != g1.N)
         return false;
     if (chain_small(g1))
