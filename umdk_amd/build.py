@@ -1,7 +1,6 @@
 """Builds libcamhip.so (the C-ABI library of HIP kernels for gfx950) in-tree.
 
     python -m umdk_amd.build              # -> umdk_amd/lib/libcamhip.so
-    python -m umdk_amd.build --timeline   # diagnostic variant -> umdk_amd/lib/timeline/libcamhip.so
 
 Every source is compiled by hipcc for gfx950 only; symbols are hidden except
 the extern "C" entry points declared in include/camhip.h.
@@ -65,12 +64,5 @@ def build(verbose=True, defines=(), lib=LIB):
     return lib
 
 
-# the diagnostic build of the grouped GEMMs' per-tile timeline (umdk_amd/timeline.py); never the shipped library
-TIMELINE_LIB = os.path.join(LIBDIR, "timeline", "libcamhip.so")
-
-
 if __name__ == "__main__":
-    if "--timeline" in sys.argv[1:]:
-        build(defines=["-DCAM_GMM_TIMELINE"], lib=TIMELINE_LIB)
-    else:
-        build()
+    build()

@@ -170,7 +170,9 @@ template <bool CO, typename T> __device__ __forceinline__ void st_h(T *p, T v)
 #ifdef CAM_GMM_TIMELINE
 constexpr int G_TL_SLOTS = 128, G_TL_BLOCKS = 1024;
 __device__ uint64_t g_cam_tl[G_TL_BLOCKS * G_TL_SLOTS][3];
-#define CAM_TL_DECL int tl_k = BM >= 256 ? 0 : BM >= 128 ? 32 : 64; uint64_t tl_t0 = wall_clock64();
+#define CAM_TL_DECL                                                                                             \
+    int tl_k = (BM >= 256 ? 0 : BM >= 128 ? 32 : 64) + (ROLE == SYNC_CONSUME ? 16 : 0);                         \
+    uint64_t tl_t0 = wall_clock64();
 #define CAM_TL_REC(e, tile)                                                                                     \
     do {                                                                                                        \
         const uint64_t tl_t1 = wall_clock64();                                                                  \
@@ -1581,16 +1583,27 @@ template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_
     (void)cp;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_SMALL_BYTES - sizeof(GroupTables));
+    // Decode tiles are weight streams of fixed size, so the two phases are balanced statically: GMM1's tiles go
+    // round-robin over every block, and the blocks left with one GMM1 tile fewer start GMM2 with a run of R
+    // tiles, R = a GMM1 tile's weight bytes over a GMM2 tile's (256 rows of K1 against 128 rows of K2).  Those
+    // first GMM2 tiles (the first experts) depend only on GMM1's first round.
+    const int pos = xcd_position(), G = gridDim.x;
+    int t1;
     {
         const GmmArgs p1 = chain_params()->g1;
         build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
                                               ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
-        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE, true>(p1, gt, -1);
+        t1 = gt->tile_end[2][p1.L - 1] * (p1.N / 2 / 128);
+        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE, true>(p1, gt, pos);
     }
     lds_sync();
     const GmmArgs p2 = chain_params()->g2;
-    const int bid = arrival_bid(p2.M, p2.L, smem);
-    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME, true>(p2, gt, -1, 0, 0, 1, bid);
+    const int r1 = t1 % G, nfree = r1 ? G - r1 : 0;
+    const bool is_free = nfree > 0 && pos >= r1;
+    constexpr int BN2 = small_bn(32, EPI_PLAIN);
+    const int R = max(1, (GBN * chain_params()->g1.K + BN2 * p2.K / 2) / (BN2 * p2.K));
+    gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME, true>(p2, gt, R * nfree + pos, is_free ? (pos - r1) * R : 0,
+                                                          is_free ? R : 0, 1);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
