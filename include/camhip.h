@@ -174,7 +174,9 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  *   [localExperts] (inclusive prefix), recvTokensPerExpert [localExperts] int64, and combineRowMap
  *   [numTokens, topK] = the row of (t,k), or -1, which replaces the combine's own scatter pass.
  *   camhipMoePrefillCombine: camhipMoeCombineNormal on those outputs (y [rows, hidden] bf16 expert outputs in
- *   dispatch order), reading combineRowMap instead of building it.
+ *   dispatch order), reading combineRowMap instead of building it.  Its localExperts and recvRowsCapacity must
+ *   be the values of the camhipMoePrefillDispatch call that produced the outputs (recvCount[localExperts - 1]
+ *   is the row total; y and expandIdx hold recvRowsCapacity rows): the call cannot check buffer sizes.
  * Limits: numTokens in [1,65536], topK <= 16, localExperts <= numExperts <= 512, recvRowsCapacity in
  * [1, numTokens * topK]. */
 CAMHIP_API camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(
@@ -198,7 +200,9 @@ CAMHIP_API camhipStatus camhipMoePrefillCombine(void *workspace, uint64_t worksp
  * GPU, held until the process ends), so numTokens * numTopk must not exceed
  * CAMHIP_COMBINE_NOALLOC_MAX_SLOTS (CAMHIP_ERROR_INVALID_PARAM otherwise).  Every call on a GPU shares
  * that scratch: calls that overlap on one GPU (other streams, other threads) race and must be
- * serialised by the caller.  No hipMalloc, hipFree or allocating library call is made. */
+ * serialised by the caller.  No hipMalloc, hipFree or allocating library call is made.  The scratch's
+ * device address is looked up once per device and kept for the process: after hipDeviceReset (or anything
+ * else that unloads the library's code objects) the entry point must not be called again in that process. */
 #define CAMHIP_COMBINE_NOALLOC_MAX_SLOTS (1L << 18)
 CAMHIP_API camhipStatus camhipMoeCombineNormalNoAlloc(const uint16_t *recvX, const int32_t *tokenSrcInfo,
                                                       int64_t numRecvRows, const int32_t *epRecvCounts,

@@ -231,3 +231,36 @@ def test_fused_rejects_operands_past_32bit_offsets(L, i2):
                          4096, 7168, 8, 4096, 0, 3, 1, 0, 32, 0, 0, P, None, P)
     assert st == 0, msg
     L.camhipReleaseExecutor(ex)
+
+
+
+@pytest.mark.parametrize("T,K,H,Lx,cap,frag", [
+    (0, 8, 1024, 8, 8, "numTokens"), (4, 8, 1024, 0, 8, "localExperts"), (4, 2, 1024, 8, 9, "recvRowsCapacity"),
+    (4, 2, 1024, 8, 0, "recvRowsCapacity"), (4, 17, 1024, 8, 8, "topK"), (4, 2, 1000, 8, 8, "hidden"),
+])
+def test_prefill_combine_rejects_out_of_range(L, T, K, H, Lx, cap, frag):
+    st, _, _, msg = _ws(L, "camhipMoePrefillCombine", P, P, P, P, P, T, K, H, Lx, cap, P)
+    assert st == 161001 and frag in msg, msg
+
+
+def test_prefill_combine_null_pointers_are_rejected(L):
+    st, _, _, msg = _ws(L, "camhipMoePrefillCombine", P, P, None, P, P, 4, 2, 1024, 8, 8, P)
+    assert st == 161002 and "combineRowMap" in msg, msg
+    st, ws, ex, msg = _ws(L, "camhipMoePrefillCombine", P, P, P, P, P, 4, 2, 1024, 8, 8, P)
+    assert st == 0 and ws == 0, msg
+    L.camhipReleaseExecutor(ex)
+
+
+@pytest.mark.parametrize("dt,H,I2,frag", [(2, 1024, 512, "dtype"), (3, 1000, 512, "k"), (3, 1024, 300, "I")])
+def test_moe_experts_rejects_bad_arguments(L, dt, H, I2, frag):
+    st, _, _, msg = _ws(L, "camhipMoeExperts", P, P, P, 8, 64, H, I2, P, P, P, P, dt, 1, P, P, P)
+    assert st == 161001 and frag in msg, msg
+
+
+def test_moe_experts_workspace_holds_the_counters(L):
+    # decode-sized groups (<= 48 rows per group): the chained launch's readiness counters, cleared by the call
+    st, ws, ex, msg = _ws(L, "camhipMoeExperts", P, P, P, 32, 1024, 7168, 4096, P, P, P, P, 3, 1, P, P, P)
+    assert st == 0 and ws >= 4 * (1024 // 32 + 32), msg
+    L.camhipReleaseExecutor(ex)
+    st, _, _, msg = _ws(L, "camhipMoeExperts", P, P, P, 32, 1024, 7168, 4096, P, P, P, P, 3, 1, P, None, P)
+    assert st != 0, "fp8 h scales are required"

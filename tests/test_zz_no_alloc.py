@@ -46,11 +46,18 @@ def test_noalloc_combine_matches_two_phase_combine(with_stats):
         ref = plan.combine(y).clone()                         # the two-phase entry point, caller workspace
         out = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device="cuda")
         stats = torch.zeros(1, dtype=torch.int32, device="cuda") if with_stats else None
+        _noalloc(plan, y, out, stats)  # warm-up: the kernels' code is loaded by the first launch
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        if stats is not None:
+            stats.zero_()
         torch.cuda.synchronize()
         before = torch.cuda.memory_allocated()
+        free_before = torch.cuda.mem_get_info()[0]  # the device's free bytes (hipMemGetInfo): any allocation
         _noalloc(plan, y, out, stats)
         torch.cuda.synchronize()
         assert torch.cuda.memory_allocated() == before
+        assert torch.cuda.mem_get_info()[0] == free_before, "device memory was allocated"
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"call {i}"
         if with_stats:
             assert int(stats.item()) >= 0

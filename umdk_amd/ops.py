@@ -297,7 +297,8 @@ def _converted(src, tag, make):
     the same weights on every step (the reference's dynamic-EPLB lists, test_fused_deep_moe.py:256-269)
     pays the copy once and keeps one stable device address (a captured graph reads it).  After the source is
     modified in place, the next eager call refreshes the copy in place (same address, so graphs captured on it
-    replay the new values from then on).  The entry is dropped when the source is freed.  A conversion first
+    replay the new values from then on; the refresh first waits for the device, so no replay in flight reads a
+    half-updated copy).  The entry is dropped when the source is freed.  A conversion first
     needed inside graph capture is refused: the copy would land in the graph's private pool."""
     key = (id(src), tag)
     ent = _CONVERTED.get(key)
@@ -307,8 +308,12 @@ def _converted(src, tag, make):
            f"fused_deep_moe: {tag} needs a converted copy (layout or dtype) that cannot be made inside graph "
            "capture; run the call once eagerly before capturing, or pass the kernels' own layout")
     if ent is not None and ent[0]() is src:
-        # the source changed in place: refresh the copy in place, so graphs captured on it see the new values
+        # the source changed in place: refresh the copy in place, so graphs captured on it see the new values.
+        # A graph replay still reading the copy may be in flight on any stream of the device: wait for the
+        # device first, so the replay never reads a half-updated weight (a rare path: weights change rarely)
         out = ent[2]
+        if out.is_cuda:
+            torch.cuda.synchronize(out.device)
         out.copy_(make())
         _CONVERTED[key] = (ent[0], src._version, out)
         return out
