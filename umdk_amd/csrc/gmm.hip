@@ -264,6 +264,9 @@ __device__ void build_group_tables(const int64_t *__restrict__ group_list, int L
 // chunk) land on 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int swz(int row, int chunk) { return row * GKB + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
+// the lane's index in its wave, from mbcnt (no work-item id register)
+__device__ __forceinline__ int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
 // s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima)
 template <int N> __device__ __forceinline__ void wait_vmcnt()
 {
@@ -357,9 +360,12 @@ constexpr int G_DYN = -2;  // gmm_body's `first` for a dynamic tile queue (see t
 // EAGER (the 4-wave chained kernel): a producer's primed tile counts its predecessor at k-step edge STAGES-2
 // instead of after its k-loop (a branch inside the k-loop, which the 8-wave kernels cannot afford).  bid: the
 // block's position for balanced placement (a chained consumer passes its arrival order), -1: blockIdx.x.
+// wv: the wave's index in the block (a scalar the kernel computes once; -1: from threadIdx.x).  The body
+// takes the lane from mbcnt and never reads the work-item id: a register holding it through the whole kernel
+// gets spilled, and each reload before a k-loop makes the loop wait for it at every iteration.
 template <int DT, int EPI, int BM, bool NTW = (BM <= CAM_GMM_NT_MAXBM), int ROLE = SYNC_NONE, bool EAGER = false>
 __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gtab, int first, int rs = 0, int rn = 0,
-                                         int rstride = 1, int bid = -1)
+                                         int rstride = 1, int bid = -1, int wv = -1)
 {
     using TC = Tile<BM, small_bn(BM, EPI)>;
     constexpr int TBN = TC::BN;
@@ -374,8 +380,9 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     auto tile_prefix = [&](int e) { return e > 0 ? tile_end[e - 1] : 0; };
     auto row_off = [&](int e) { return e > 0 ? gtab->row_end[e - 1] : 0; };
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = lane_id();
+    const int w = wv >= 0 ? wv : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const bool first_thread = w == 0 && lane == 0;
     const int wm = w / TC::WAVES_N, wn = w % TC::WAVES_N;
     const int l16 = lane & 15, lg = lane >> 4;
     constexpr bool PRODUCE = ROLE == SYNC_PRODUCE, CONSUME = ROLE == SYNC_CONSUME;
@@ -739,13 +746,13 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
     auto SY = [&]() -> GmmSync { return chain_params()->sy; };  // (chained kernels only)
     // the counter of a tile's M-tile, from its context
     auto mti_ctx = [&](const Ctx &c) {
-        return cls_base() + tile_prefix(c.e) + (c.row0 - row_off(c.e)) / GBM;
+        return __builtin_amdgcn_readfirstlane(cls_base() + tile_prefix(c.e) + (c.row0 - row_off(c.e)) / GBM);
     };
     int sig = -1;      // producer: counter of the tile whose stores are still to be counted
     int gave_up = 0;   // consumer: a wait of this wave gave up (the launch's outputs are void; no more waits)
     auto signal = [&]() {
         if constexpr (PRODUCE) {
-            if (sig >= 0 && threadIdx.x == 0)
+            if (sig >= 0 && first_thread)
                 __hip_atomic_fetch_add(gptr(SY().ready + sig), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sig = -1;
         }
@@ -788,7 +795,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
         const int mt_e = tile_end[e] - tile_prefix(e);
         const int grp = local / (GM * ntn), rem = local % (GM * ntn);
         const int gm = min(GM, mt_e - grp * GM);
-        return cls_base() + tile_prefix(e) + grp * GM + rem % gm;
+        return __builtin_amdgcn_readfirstlane(cls_base() + tile_prefix(e) + grp * GM + rem % gm);
     };
 
     if constexpr (BM >= 256) {
@@ -830,14 +837,14 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             return 0;
         };
         auto publish = [&](int k) {
-            if (threadIdx.x == 0)
+            if (first_thread)
                 *qslot = k < rn ? rs + k : total;
             lds_sync();
             return __builtin_amdgcn_readfirstlane(*qslot);
         };
         int kt = 0, tile;
         if (dyn) {
-            const int k = threadIdx.x == 0 ? take() : 0;
+            const int k = first_thread ? take() : 0;
             tile = publish(k);
         } else {
             tile = seq(0);
@@ -981,7 +988,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
             if (dyn) {
                 // the queue's answer arrives while the ring drains; then the next tile's counter, answered
                 // during the epilogue
-                const int k = threadIdx.x == 0 ? take() : 0;
+                const int k = first_thread ? take() : 0;
                 wait_vmcnt<0>();
                 ntile = publish(k);
                 if (ntile < total && !gave_up)
@@ -1112,7 +1119,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 // the next tile's counter (bar() is a compiler memory barrier: the slot is read afresh), then
                 // the copy of the one after it into the slot this tile's counter occupied
                 if (chain)
-                    chain = rslot[(kt & 1) * 64] >= SY().target;
+                    chain = __builtin_amdgcn_readfirstlane(rslot[(kt & 1) * 64]) >= SY().target;
                 const int t2 = seq(kt + 1);
                 if (t2 < total && w == 0)
                     dma4_sc1(SY().ready + mti_of(t2), rslot + ((kt + 1) & 1) * 64);
@@ -1135,7 +1142,7 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         if (edge == e_copy && w == 0)
                             dma4_sc1(SY().ready + mti_ctx(nxt), scratch);
                         if (edge == e_read)
-                            chain = scratch[0] >= SY().target;  // (bar() is a compiler memory barrier)
+                            chain = __builtin_amdgcn_readfirstlane(scratch[0]) >= SY().target;  // (bar(): read afresh)
                     }
                 }
                 if constexpr (EAGER)
@@ -1363,9 +1370,10 @@ template <int DT, int EPI> __global__ __launch_bounds__(256, 1) void gmm_kernel_
 {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_SMALL_BYTES - sizeof(GroupTables));
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     build_group_tables<Tile<32>::THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem),
                                           ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
-    gmm_body<DT, EPI, 32>(p, gt, -1);
+    gmm_body<DT, EPI, 32>(p, gt, -1, 0, 0, 1, -1, wv);
 }
 
 // Prefill: 8 waves, 128- or 256-row tile picked per launch from the actual rows per touched
@@ -1415,13 +1423,13 @@ template <int DT> __device__ __forceinline__ ClassRanges big_ranges(bool tall)
 // bid: the block's id for the placement (blockIdx.x; a chained consumer passes its arrival order, so that the
 // blocks that finish GMM1 first take the positions with the most GMM2 work).
 template <int DT, int EPI, int ROLE>
-__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall, int bid)
+__device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables *gt, bool tall, int bid, int wv)
 {
     const int pos = (gridDim.x & 7) ? bid : (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);  // XCD-aware order
     constexpr int SMALL = DT == DT_INT8 ? 1 : G_SMALL_ROWS;  // rows below: the 32-row tile class
     constexpr bool KEEP = ROLE != SYNC_NONE;
     if (!tall) {
-        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1, bid);
+        gmm_body<DT, EPI, 128, false, ROLE>(p, gt, -1, 0, 0, 1, bid, wv);
         return;
     }
     // light tiles worth about one heavy tile: a 256-row tile against 128-row tiles (2 for 1-byte operands, 1
@@ -1429,8 +1437,11 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
     // heavy tile against 9 and 45-55 us per light one)
     constexpr int run = DT == DT_BF16 ? 1 : 2;
     constexpr int run32 = EPI == EPI_PLAIN ? 4 : CAM_GMM_RUN32;
-    const int n_heavy = gt->tile_end[0][p.L - 1];  // 256-row M-tiles of the heavy experts
-    const bool has_mid = gt->tile_end[1][p.L - 1] > 0, has_small = gt->tile_end[2][p.L - 1] > 0;
+    // (uniform values read from LDS go to scalar registers at once: a VGPR holding one across the classes gets
+    // spilled, and its reload after a tile's k-loop makes the next k-loop wait for it at every iteration)
+    const int n_heavy = __builtin_amdgcn_readfirstlane(gt->tile_end[0][p.L - 1]);  // 256-row M-tiles (heavy)
+    const bool has_mid = __builtin_amdgcn_readfirstlane(gt->tile_end[1][p.L - 1]) > 0;
+    const bool has_small = __builtin_amdgcn_readfirstlane(gt->tile_end[2][p.L - 1]) > 0;
     const int G = gridDim.x;
     // 256-row tiles: heavy M-tiles x N-tiles
     const int heavy_tiles = n_heavy * (EPI != EPI_PLAIN ? p.N / 2 / 128 : p.N / 256);
@@ -1442,15 +1453,15 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
             const int nq = (G & 7) ? 1 : 8, x = nq == 1 ? 0 : (bid & 7);
             const int hx = (heavy_tiles + nq - 1) / nq;
             const int len = max(0, min(hx, heavy_tiles - x * hx));
-            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, G_DYN, x * hx, len, chain_queue_index(p.M, p.L) + x);
+            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, G_DYN, x * hx, len, chain_queue_index(p.M, p.L) + x, -1, wv);
             lds_sync();
         }
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, pos, 0, 0, 1);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, pos, 0, 0, 1, -1, wv);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, pos, 0, 0, 1);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, pos, 0, 0, 1, -1, wv);
             }
         }
         return;
@@ -1466,7 +1477,7 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         auto heavy_in = [&](int x) { return max(0, min(hx, heavy_tiles - x * hx)); };
         const int len = heavy_in(xcd);
         if (slot < len) {
-            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, 0x3fffffff, xcd * hx + slot, (len - slot + S - 1) / S, S);
+            gmm_body<DT, EPI, 256, false, ROLE>(p, gt, 0x3fffffff, xcd * hx + slot, (len - slot + S - 1) / S, S, -1, wv);
             lds_sync();  // every wave is done with the first class's ring
         }
         int free_before = 0, free_all = 0;
@@ -1478,28 +1489,26 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
         const bool is_free = slot >= len;
         const int fpos = free_before + slot - len;  // the block's rank among the free blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + bid, is_free ? fpos * run : 0,
-                                               is_free ? run : 0, 1);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * free_all + bid, is_free ? fpos * run : 0, is_free ? run : 0, 1, -1, wv);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
-                if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
+                if (!KEEP && wv >= Tile<32>::NWAVES)
                     return;  // the 32-row tile's four waves go on (a barrier only counts the waves still running)
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + bid,
-                                                  is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * free_all + bid, is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1, -1, wv);
             }
         }
         return;
     }
     if (n_heavy == 0) {  // one class after another, each balanced over the blocks
         if (has_mid)
-            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1, bid);
+            gmm_body<DT, EPI, 128, true, ROLE>(p, gt, -1, 0, 0, 1, bid, wv);
         if constexpr (SMALL > 1) {
             if (has_small) {
                 lds_sync();
-                if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
+                if (!KEEP && wv >= Tile<32>::NWAVES)
                     return;
-                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1, bid);
+                gmm_body<DT, EPI, 32, true, ROLE>(p, gt, -1, 0, 0, 1, bid, wv);
             }
         }
         return;
@@ -1509,21 +1518,20 @@ __device__ __forceinline__ void big_schedule(const GmmArgs &p, const GroupTables
     // light tiles with a run of about one heavy tile's worth each; the rest of the light tiles go
     // round-robin over all blocks (measured on config 4's GMM2, 364 heavy tiles on 256 blocks: the light
     // tiles' round-robin then no longer lands on blocks still busy with their second heavy tile).
-    gmm_body<DT, EPI, 256, false, ROLE>(p, gt, pos, 0, 0, 1);
+    gmm_body<DT, EPI, 256, false, ROLE>(p, gt, pos, 0, 0, 1, -1, wv);
     lds_sync();  // every wave is done with the first class's ring
     const int r = heavy_tiles % G;
     const int nfree = r > 0 ? G - r : 0;
     const bool is_free = nfree > 0 && pos >= r;
     const int fpos = pos - r;
     if (has_mid)
-        gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * nfree + pos, is_free ? fpos * run : 0, is_free ? run : 0, 1);
+        gmm_body<DT, EPI, 128, true, ROLE>(p, gt, run * nfree + pos, is_free ? fpos * run : 0, is_free ? run : 0, 1, -1, wv);
     if constexpr (SMALL > 1) {
         if (has_small) {
             lds_sync();
-            if (!KEEP && threadIdx.x >= Tile<32>::THREADS)
+            if (!KEEP && wv >= Tile<32>::NWAVES)
                 return;
-            gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0,
-                                              is_free ? run32 : 0, 1);
+            gmm_body<DT, EPI, 32, true, ROLE>(p, gt, run32 * nfree + pos, is_free ? fpos * run32 : 0, is_free ? run32 : 0, 1, -1, wv);
         }
     }
 }
@@ -1532,10 +1540,11 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
 {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const bool tall = big_tall(p.allow256, p.K, DT);
     // every class's expert table, from one read of the counts
     build_group_tables<GMAX_THREADS>(p.group_list, p.L, *gt, reinterpret_cast<int *>(smem), big_ranges<DT>(tall));
-    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall, (int)blockIdx.x);
+    big_schedule<DT, EPI, SYNC_NONE>(p, gt, tall, (int)blockIdx.x, wv);
 }
 
 // Chained GMM1 + SwiGLU -> GMM2 (launch_gmm_chain): one table build, every block's GMM1 tiles (producing), then
@@ -1546,11 +1555,11 @@ template <int DT, int EPI> __global__ __launch_bounds__(512, 1) void gmm_kernel_
 // The block's arrival order at the GMM1 -> GMM2 boundary, as a block id: its rank among the blocks of its XCD
 // (one counter per XCD, after the M-tile counters) in place of blockIdx.x >> 3.  The consumer phase places its
 // tiles by it: the blocks that finish GMM1 first take the positions that hold the most GMM2 work.
-__device__ __forceinline__ int arrival_bid(int M, int L, uint8_t *smem)
+__device__ __forceinline__ int arrival_bid(int M, int L, uint8_t *smem, int wv)
 {
     int *slot = reinterpret_cast<int *>(smem);  // the ring is idle between the phases
     const int xcd = blockIdx.x & 7;
-    if (threadIdx.x == 0) {
+    if (wv == 0 && lane_id() == 0) {
         int *ctr = chain_params()->sy.ready + chain_arrival_index(M, L) + xcd;
         *slot = __hip_atomic_fetch_add(gptr(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1565,18 +1574,19 @@ template <int DT, int EPI1> __global__ __launch_bounds__(512, 1) void gmm_chain_
     (void)cp;  // read through chain_params()
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     GroupTables *gt = reinterpret_cast<GroupTables *>(smem + G_LDS_BIG_BYTES - sizeof(GroupTables));
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     bool tall;
     {
         const GmmArgs p1 = chain_params()->g1;
         tall = big_tall(p1.allow256, p1.K, DT);  // the host checked that GMM2 makes the same choice
         build_group_tables<GMAX_THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
                                          big_ranges<DT>(tall));
-        big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall, (int)blockIdx.x);
+        big_schedule<DT, EPI1, SYNC_PRODUCE>(p1, gt, tall, (int)blockIdx.x, wv);
     }
     lds_sync();  // every wave is done with GMM1's last ring
     const GmmArgs p2 = chain_params()->g2;
-    const int bid = arrival_bid(p2.M, p2.L, smem);
-    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall, bid);
+    const int bid = arrival_bid(p2.M, p2.L, smem, wv);
+    big_schedule<DT, EPI_PLAIN, SYNC_CONSUME>(p2, gt, tall, bid, wv);
 }
 template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_small(ChainParams cp)
 {
@@ -1588,13 +1598,14 @@ template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_
     // tiles, R = a GMM1 tile's weight bytes over a GMM2 tile's (256 rows of K1 against 128 rows of K2).  Those
     // first GMM2 tiles (the first experts) depend only on GMM1's first round.
     const int pos = xcd_position(), G = gridDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     int t1;
     {
         const GmmArgs p1 = chain_params()->g1;
         build_group_tables<Tile<32>::THREADS>(p1.group_list, p1.L, *gt, reinterpret_cast<int *>(smem),
                                               ClassRanges{{0, 0, 0}, {0, 0, 0x7fffffff}});
         t1 = gt->tile_end[2][p1.L - 1] * (p1.N / 2 / 128);
-        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE, true>(p1, gt, pos);
+        gmm_body<DT, EPI1, 32, true, SYNC_PRODUCE, true>(p1, gt, pos, 0, 0, 1, -1, wv);
     }
     lds_sync();
     const GmmArgs p2 = chain_params()->g2;
@@ -1603,7 +1614,7 @@ template <int DT, int EPI1> __global__ __launch_bounds__(256, 1) void gmm_chain_
     constexpr int BN2 = small_bn(32, EPI_PLAIN);
     const int R = max(1, (GBN * chain_params()->g1.K + BN2 * p2.K / 2) / (BN2 * p2.K));
     gmm_body<DT, EPI_PLAIN, 32, true, SYNC_CONSUME, true>(p2, gt, R * nfree + pos, is_free ? (pos - r1) * R : 0,
-                                                          is_free ? R : 0, 1);
+                                                          is_free ? R : 0, 1, -1, wv);
 }
 
 // Per-device launch state: the CU count and whether a kernel's dynamic-LDS limit has been raised.
