@@ -19,6 +19,7 @@
 // Entries whose expert id is outside [0,E) are skipped.
 #include "cam_device.h"
 #include "launchers.h"
+#include "prefill_dev.h"
 
 namespace cam {
 
@@ -26,44 +27,8 @@ constexpr int DISP_WAVES = 4;
 constexpr int DISP_NIT = 7;  // H <= 7168 = 7 * 1024
 constexpr int DISP_MAX_K = 16;
 
-// Where the rank of (t,k) within its expert comes from: send_token_idx[t,k] (the layout op's output), or,
-// with send_token_idx == nullptr, chunk_base (the prefill step: chunks of `tpc` tokens, chunk_base[e * nc + c]
-// = entries of expert e in chunks before c) plus chunk_rank[t,k], the rank inside the chunk (the routing
-// kernel's).
-struct RankSrc {
-    const int32_t *send_token_idx;
-    const int32_t *chunk_base;
-    const int32_t *chunk_rank;
-    int tpc;
-};
-
-// Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
-__device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
-                                             const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
-                                             int T, int K, int E, int cap, int lane)
-{
-    int dst = -1;
-    if (topk_idx == nullptr)  // identity mode (K = 1): row t of x quantised into row t
-        return lane == 0 ? t : -1;
-    if (rs.send_token_idx) {
-        if (lane < K) {
-            const int e = topk_idx[(size_t)t * K + lane];
-            if (e >= 0 && e < E)
-                dst = send_offset[e] + rs.send_token_idx[(size_t)t * K + lane];
-        }
-    } else if (lane < K) {
-        const int e = topk_idx[(size_t)t * K + lane];
-        if (e >= 0 && e < E) {
-            const int nc = (T + rs.tpc - 1) / rs.tpc;
-            dst = send_offset[e] + rs.chunk_base[(size_t)e * nc + t / rs.tpc] + rs.chunk_rank[(size_t)t * K + lane];
-        }
-    }
-    if (dst >= cap)  // inconsistent counts: never write outside the output
-        dst = -1;
-    return dst < 0 ? -1 : dst;
-}
-
-// bf16 copy and fp8 1x128 quantisation: one wave per (token, 1024-column chunk).
+// bf16 copy and fp8 1x128 quantisation: one wave per (token, 1024-column chunk) (dispatch_wave in
+// prefill_dev.h).
 template <int MODE>
 __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx, const int32_t *__restrict__ send_offset,
@@ -71,100 +36,12 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     uint8_t *__restrict__ expand_x, float *__restrict__ scales, int32_t *__restrict__ expand_idx,
     int32_t *__restrict__ inv_out, int kmajor, int skip_unrouted)
 {
-#pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
     const long item = (long)blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
     if (item >= (long)T * nchunk)
         return;
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
-    // skip_unrouted (a rank holding some of the experts): a token none of whose picks is an expert of this rank
-    // reads nothing, only its row-map entries are written (config 4, 32 of 256 experts local: 40% of the
-    // tokens, the layer 2-3 us faster; with every expert local the check measured 0.7 us slower per step)
-    if (skip_unrouted && topk_idx) {
-        const int e0 = lane < K ? topk_idx[(size_t)t * K + lane] : -1;
-        if (__ballot(e0 >= 0 && e0 < E) == 0) {
-            if (inv_out && j == 0 && lane < K)
-                inv_out[(size_t)t * K + lane] = -1;
-            return;
-        }
-    }
-    // the slice of x is requested first, so its loads are in flight while the destination rows resolve
-    if constexpr (MODE == QUANT_NONE) {
-        // lane l copies columns [1024 j + 8 l, +8) and [1024 j + 512 + 8 l, +8): each 16-byte
-        // store instruction of the wave writes one contiguous kilobyte
-        const int col = j * 1024 + lane * 8;
-        const bool act = col < H, act1 = col + 512 < H;
-        u32x4 raw0 = u32x4{0, 0, 0, 0}, raw1 = u32x4{0, 0, 0, 0};
-        if (act) {
-            raw0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col));
-            if (act1)
-                raw1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col + 512));
-        }
-        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
-        if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
-            inv_out[(size_t)t * K + lane] = dst;
-        for (int k = 0; k < K; ++k) {
-            const int row = __shfl(dst, k, 64);
-            if (row < 0)
-                continue;
-            if (act) {
-                uint16_t *out = reinterpret_cast<uint16_t *>(expand_x) + (size_t)row * H + col;
-                *reinterpret_cast<u32x4 *>(out) = raw0;
-                if (act1)
-                    *reinterpret_cast<u32x4 *>(out + 512) = raw1;
-            }
-            if (j == 0 && lane == 0 && expand_idx) {
-                expand_idx[(size_t)row * 3 + 0] = rank;
-                expand_idx[(size_t)row * 3 + 1] = t;
-                expand_idx[(size_t)row * 3 + 2] = k;
-            }
-        }
-    } else {
-        // lane l quantises columns [1024 j + 16 l, +16): one 16-byte fp8 store per row.  Cached loads of x
-        // and streaming (nontemporal) stores of the rows: measured 5% faster on the DSV3 rank shape than the
-        // reverse (nontemporal loads, cached stores), and 11% faster than cached loads and stores.
-        const int col = j * 1024 + lane * 16;
-        const bool act = col < H;
-        u32x4 raw0 = u32x4{0, 0, 0, 0}, raw1 = u32x4{0, 0, 0, 0};
-        if (act) {
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)t * H + col);
-            raw0 = src[0];
-            raw1 = src[1];
-        }
-        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
-        if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
-            inv_out[(size_t)t * K + lane] = dst;
-        float f[16];
-        unpack_bf16x8(raw0, f);
-        unpack_bf16x8(raw1, f + 8);
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            amax = fmaxf(amax, fabsf(f[i]));
-        amax = fmaxf(group_max<8>(amax), 1e-4f);  // a 128-block is 8 adjacent lanes
-        const float inv = 448.0f / amax;
-        const float bscale = amax / 448.0f;
-        u32x4 q;
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-            q[w] = f32x4_to_e4m3(f[4 * w] * inv, f[4 * w + 1] * inv, f[4 * w + 2] * inv, f[4 * w + 3] * inv);
-        const int nb = H >> 7;
-        for (int k = 0; k < K; ++k) {
-            const int row = __shfl(dst, k, 64);
-            if (row < 0)
-                continue;
-            if (act) {
-                __builtin_nontemporal_store(q, reinterpret_cast<u32x4 *>(expand_x + (size_t)row * H + col));
-                if ((lane & 7) == 0)
-                    scales[kmajor ? (size_t)(col >> 7) * cap + row : (size_t)row * nb + (col >> 7)] = bscale;
-            }
-            if (j == 0 && lane == 0 && expand_idx) {
-                expand_idx[(size_t)row * 3 + 0] = rank;
-                expand_idx[(size_t)row * 3 + 1] = t;
-                expand_idx[(size_t)row * 3 + 2] = k;
-            }
-        }
-    }
+    dispatch_wave<MODE, false>(x, topk_idx, send_offset, rs, t, j, T, H, K, E, rank, cap, expand_x, scales,
+                               expand_idx, inv_out, kmajor, skip_unrouted, [] {});
 }
 
 // int8 per-token quantisation needs the whole row's amax: one wave per token,
@@ -187,7 +64,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const int t = blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
     if (t >= T)
         return;
-    const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+    const int dst = dispatch_dest<false>(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
     if (inv_out && lane < K)
         inv_out[(size_t)t * K + lane] = dst;
     const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)t * H);

@@ -18,6 +18,7 @@
 // Expert ids outside [0,E) are not routed: send_token_idx = -1, not counted.
 #include "cam_device.h"
 #include "launchers.h"
+#include "prefill_dev.h"
 
 namespace cam {
 
@@ -190,10 +191,7 @@ __global__ __launch_bounds__(RANK_THREADS) void layout_rank_kernel(const IdxT *_
 
 // The prefill step's bookkeeping after route_kernel<.., HIST> (chunks of 16 tokens): one wave per local
 // expert (four per block, all blocks in parallel: a single block would be bound by one CU's outstanding
-// memory requests) scans the expert's row of chunk counts in place into exclusive chunk bases, and sums the
-// expert's row of chunk prefixes (each chunk's count of the lower experts' picks) into its send offset, so
-// every expert's count exchange entry is known without a second pass over the totals: send_offset =
-// exclusive, recv_count = inclusive prefix over the experts, tokens_per_expert as int64.
+// memory requests) runs scan_expert (prefill_dev.h): chunk bases in place, send offset, count exchange.
 constexpr int SN_THREADS = 256;
 constexpr int SN_WAVES = SN_THREADS / 64;
 __global__ __launch_bounds__(SN_THREADS) void scan_notify_kernel(int E, int nc, int32_t *__restrict__ counts,
@@ -202,53 +200,10 @@ __global__ __launch_bounds__(SN_THREADS) void scan_notify_kernel(int E, int nc, 
                                                                  int32_t *__restrict__ recv_count,
                                                                  int64_t *__restrict__ tokens_per_expert)
 {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int e = blockIdx.x * SN_WAVES + w;
+    const int e = blockIdx.x * SN_WAVES + (int)(threadIdx.x >> 6);
     if (e >= E)
         return;
-    int32_t *row = counts + (size_t)e * nc;
-    const int32_t *prow = pref + (size_t)e * nc;
-    int32_t pre[4], pp[4];  // the first 256 chunks' counts and prefixes in flight together
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const bool in = u * 64 + lane < nc;
-        pre[u] = in ? row[u * 64 + lane] : 0;
-        pp[u] = in ? prow[u * 64 + lane] : 0;
-    }
-    int32_t carry = 0, below = 0;
-    for (int c0 = 0; c0 < nc; c0 += 64) {
-        const int c = c0 + lane;
-        int32_t v = 0, b = 0;
-        if (c0 < 256) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                v = c0 == u * 64 ? pre[u] : v;
-                b = c0 == u * 64 ? pp[u] : b;
-            }
-        } else if (c < nc) {
-            v = row[c];
-            b = prow[c];
-        }
-        int32_t incl = v;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int32_t u = __shfl_up(incl, o, 64);
-            if (lane >= o)
-                incl += u;
-        }
-        if (c < nc)
-            row[c] = carry + incl - v;
-        carry += __shfl(incl, 63, 64);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1)
-            b += __shfl_xor(b, o, 64);
-        below += b;
-    }
-    if (lane == 0) {
-        send_offset[e] = below;
-        recv_count[e] = below + carry;
-        tokens_per_expert[e] = carry;
-    }
+    scan_expert<false>(e, nc, counts, pref, send_offset, recv_count, tokens_per_expert);
 }
 
 hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pref, int32_t *send_offset,

@@ -1,0 +1,265 @@
+// The prefill step's route -> chunk scan + count exchange -> dispatch (R0, D1, D2, D3 + Q1) in one launch.
+//
+// The grid's blocks take roles by index: the first ceil(T/16) route a 16-token chunk each (route_block), the
+// next ceil(Ec/4) scan one expert per wave (scan_expert), the rest dispatch one (token, 1024-column chunk)
+// per wave (dispatch_wave).  Blocks start in index order on every XCD, so the route and scan blocks are
+// resident before any dispatch block waits for them.  A dispatch wave issues its loads of x first and only then
+// waits for the routing and the scan, so the routing's latency, the scan's and the two launch gaps of the
+// three-launch step overlap with the first resident dispatch waves' reads of x.  The stages' results are
+// bit-identical to the three launches: the same device bodies run, their cross-stage outputs stored and read
+// agent-coherently.
+//
+// Readiness: a static per-device array of counters -- route blocks done, experts scanned, dispatch waves past
+// their wait -- published after each stage's stores have completed (vmcnt(0), then an agent-scope atomic).
+// The last dispatch wave past its wait resets all three, so every launch starts from zero (the array is zero
+// when the library is loaded).  Launches that overlap on one GPU therefore race (the reference's prefill ops
+// do not support concurrent use either, doc/en/cam/CAM API Guide.md:38-39).  A wait gives up after a bound
+// (2 s), sets the status word and lets the launch end; the host reads it with step_status_read.
+#include <atomic>
+#include <cstdlib>
+#include <mutex>
+
+#include "cam_device.h"
+#include "launchers.h"
+#include "prefill_dev.h"
+
+namespace cam {
+
+// [0] route blocks done, [1] experts scanned, [2] dispatch waves past their wait, [3] status (1: a wait gave up)
+static __device__ __align__(256) int step_sync[64];
+
+struct StepArgs {
+    const float *logits;
+    const float *bias;
+    const uint16_t *x;
+    int T, H, E, Ec, K, cap, nchunk, kmajor, skip_unrouted;
+    int32_t *topk_idx;
+    float *topk_w;
+    int32_t *counts, *pref, *chunk_rank, *send_offset, *recv_count;
+    int64_t *tokens_per_expert;
+    uint8_t *expand_x;
+    float *scales;
+    int32_t *expand_idx, *inv;
+    int nroute, nscan, ndisp_waves;
+    int extra;  // added to the wait targets: 1 makes every wait give up (a test hook)
+    int *sync;
+    long long ticks;
+};
+
+// Waits until *ctr >= target (lane 0 polls, agent-coherent); false when the bound ran out (status set).
+__device__ __forceinline__ bool step_wait(int *ctr, int target, long long ticks, int *status, int sleep_units)
+{
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+        int v = 0;
+        if ((threadIdx.x & 63) == 0)
+            v = __hip_atomic_load(gp(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(v) >= target)
+            return true;
+        if ((long long)(wall_clock64() - t0) > ticks) {
+            if ((threadIdx.x & 63) == 0)
+                __hip_atomic_fetch_or(gp(status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        if (sleep_units >= 8)
+            __builtin_amdgcn_s_sleep(8);
+        else
+            __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step_kernel(StepArgs a)
+{
+    const int b = blockIdx.x;
+    int *routed = a.sync, *scanned = a.sync + 1, *passed = a.sync + 2, *status = a.sync + 3;
+    if (b < a.nroute) {
+        route_block<PER, true, true>(a.logits, a.bias, a.T, a.E, a.K, a.topk_idx, a.topk_w, nullptr, a.Ec, a.counts,
+                                     a.pref, a.chunk_rank, b, a.nroute);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores have completed
+        __syncthreads();                 // ... every wave's
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(gp(routed), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (b < a.nroute + a.nscan) {
+        const int e = (b - a.nroute) * 4 + (int)(threadIdx.x >> 6);
+        if (e >= a.Ec)
+            return;
+        step_wait(routed, a.nroute + a.extra, a.ticks, status, 2);
+        scan_expert<true>(e, a.nroute, a.counts, a.pref, a.send_offset, a.recv_count, a.tokens_per_expert);
+        __builtin_amdgcn_s_waitcnt(0);
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_fetch_add(gp(scanned), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const long item = (long)(b - a.nroute - a.nscan) * 4 + (threadIdx.x >> 6);
+    const bool valid = item < (long)a.ndisp_waves;  // (only the last block can hold waves past the end)
+    // Wave 0 waits for the routing and the scan for the whole block (a few thousand resident waves polling one
+    // line would slow the stages they wait for), then the block meets.  Past the wait a wave reads no counter
+    // again: it counts itself, and the last one resets the counters.
+    auto ready = [&]() {
+        if (threadIdx.x < 64) {
+            if (step_wait(routed, a.nroute + a.extra, a.ticks, status, 8))
+                step_wait(scanned, a.Ec + a.extra, a.ticks, status, 8);
+        }
+        __syncthreads();
+        if (valid && (threadIdx.x & 63) == 0) {
+            const int n = __hip_atomic_fetch_add(gp(passed), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (n == a.ndisp_waves - 1) {
+                __hip_atomic_store(gp(routed), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(gp(scanned), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(gp(passed), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    };
+    if (!valid) {
+        ready();  // meets the block's barrier
+        return;
+    }
+    const int t = (int)(item / a.nchunk), j = (int)(item % a.nchunk);
+    const RankSrc rs{nullptr, a.counts, a.chunk_rank, ROUTE_WAVES * 4};
+    dispatch_wave<MODE, true>(a.x, a.topk_idx, a.send_offset, rs, t, j, a.T, a.H, a.K, a.Ec, 0, a.cap, a.expand_x,
+                              a.scales, a.expand_idx, a.inv, a.kmajor, a.skip_unrouted, ready);
+}
+
+// The array's device address on the current device, looked up once per device (host code never uses the
+// array's name as an address)
+static hipError_t step_sync_ptr(int **out)
+{
+    constexpr int MAXD = 64;
+    static std::atomic<void *> cache[MAXD];
+    static std::mutex mu;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= MAXD)
+        return hipErrorInvalidDevice;
+    void *p = cache[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(mu);
+        p = cache[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(step_sync));
+            if (e != hipSuccess)
+                return e;
+            cache[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = (int *)p;
+    return hipSuccess;
+}
+
+// CAMHIP_STEP_FUSED=0 in the environment selects the three-launch step (for measuring one against the other)
+bool step_fused_enabled()
+{
+    static const bool on = [] {
+        const char *v = getenv("CAMHIP_STEP_FUSED");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+static std::atomic<long long> g_step_ticks{0};
+static std::atomic<int> g_step_unreach{0};
+void step_debug_set(long long wait_ticks, int unreachable)
+{
+    g_step_ticks.store(wait_ticks, std::memory_order_relaxed);
+    g_step_unreach.store(unreachable ? 1 : 0, std::memory_order_relaxed);
+}
+
+hipError_t step_status_read(int *status, bool clear)
+{
+    int *p = nullptr;
+    hipError_t e = step_sync_ptr(&p);
+    if (e != hipSuccess)
+        return e;
+    int v = 0;
+    e = hipMemcpy(&v, p + 3, sizeof(int), hipMemcpyDeviceToHost);
+    if (e != hipSuccess)
+        return e;
+    if (clear && v) {
+        // a wait that gave up leaves the counters in an unknown state: start the next launch from zero
+        int zero[4] = {0, 0, 0, 0};
+        e = hipMemcpy(p, zero, sizeof(zero), hipMemcpyHostToDevice);
+        if (e != hipSuccess)
+            return e;
+    }
+    *status = v;
+    return hipSuccess;
+}
+
+hipError_t launch_prefill_step(const float *logits, const float *bias, const uint16_t *x, int T, int H, int E, int Ec,
+                               int K, int quant_mode, int cap, bool kmajor, bool skip_unrouted, int32_t *topk_idx,
+                               float *topk_w, int32_t *counts, int32_t *pref, int32_t *chunk_rank,
+                               int32_t *send_offset, int32_t *recv_count, int64_t *tokens_per_expert,
+                               void *expand_x, float *scales, int32_t *expand_idx, int32_t *inv, hipStream_t s)
+{
+    if (T < 1 || E > 16 * ROUTE_MAX_PER_LANE || K > 16 || Ec < 1 || Ec > E || H > 7 * 1024 || (H & 15))
+        return hipErrorInvalidValue;
+    if (quant_mode != QUANT_NONE && quant_mode != QUANT_FP8_BLOCK)
+        return hipErrorNotSupported;
+    if (quant_mode == QUANT_FP8_BLOCK && (H & 127))
+        return hipErrorInvalidValue;
+    int *sync = nullptr;
+    hipError_t e = step_sync_ptr(&sync);
+    if (e != hipSuccess)
+        return e;
+    StepArgs a{};
+    a.logits = logits;
+    a.bias = bias;
+    a.x = x;
+    a.T = T;
+    a.H = H;
+    a.E = E;
+    a.Ec = Ec;
+    a.K = K;
+    a.cap = cap;
+    a.nchunk = (H + 1023) / 1024;
+    a.kmajor = kmajor ? 1 : 0;
+    a.skip_unrouted = skip_unrouted ? 1 : 0;
+    a.topk_idx = topk_idx;
+    a.topk_w = topk_w;
+    a.counts = counts;
+    a.pref = pref;
+    a.chunk_rank = chunk_rank;
+    a.send_offset = send_offset;
+    a.recv_count = recv_count;
+    a.tokens_per_expert = tokens_per_expert;
+    a.expand_x = (uint8_t *)expand_x;
+    a.scales = scales;
+    a.expand_idx = expand_idx;
+    a.inv = inv;
+    a.nroute = (T + ROUTE_WAVES * 4 - 1) / (ROUTE_WAVES * 4);
+    a.nscan = (Ec + 3) / 4;
+    a.ndisp_waves = T * a.nchunk;
+    a.sync = sync;
+    a.extra = g_step_unreach.load(std::memory_order_relaxed);
+    const long long tk = g_step_ticks.load(std::memory_order_relaxed);
+    a.ticks = tk > 0 ? tk : 200000000LL;  // 2 s of the 100 MHz constant clock
+    const unsigned grid = (unsigned)(a.nroute + a.nscan + (a.ndisp_waves + 3) / 4);
+    const int per = (E + 15) >> 4;
+#define STEP_CASE(P)                                                                                                \
+    do {                                                                                                            \
+        if (quant_mode == QUANT_FP8_BLOCK)                                                                          \
+            hipLaunchKernelGGL((prefill_step_kernel<P, QUANT_FP8_BLOCK>), dim3(grid), dim3(256), 0, s, a);          \
+        else                                                                                                        \
+            hipLaunchKernelGGL((prefill_step_kernel<P, QUANT_NONE>), dim3(grid), dim3(256), 0, s, a);               \
+    } while (0)
+    if (per <= 1)
+        STEP_CASE(1);
+    else if (per <= 2)
+        STEP_CASE(2);
+    else if (per <= 4)
+        STEP_CASE(4);
+    else if (per <= 8)
+        STEP_CASE(8);
+    else if (per <= 16)
+        STEP_CASE(16);
+    else
+        STEP_CASE(32);
+#undef STEP_CASE
+    return hipGetLastError();
+}
+
+}  // namespace cam
