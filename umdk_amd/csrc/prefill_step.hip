@@ -9,9 +9,13 @@
 // bit-identical to the three launches: the same device bodies run, their cross-stage outputs stored and read
 // agent-coherently.
 //
-// Readiness: a static per-device array of counters -- route blocks done, experts scanned, dispatch waves past
+// Readiness: a static per-device array of counters -- route blocks done, experts scanned, dispatch blocks past
 // their wait -- published after each stage's stores have completed (vmcnt(0), then an agent-scope atomic).
-// The last dispatch wave past its wait resets all three, so every launch starts from zero (the array is zero
+// Device-scope atomics on one address serialise (~30 ns each: one counter bumped by each of 7168 dispatch
+// blocks measured 0.9 ms), so every counter is split into shards on cache lines of their own: 8 for the route
+// blocks and 8 for the scan waves (a waiter sums them), 64 for the dispatch blocks, whose completing blocks
+// bump one top counter.  Dispatch blocks wait for the scan only (every scan wave waited for the routing).  The
+// block that completes the top counter resets everything, so every launch starts from zero (the array is zero
 // when the library is loaded).  Launches that overlap on one GPU therefore race (the reference's prefill ops
 // do not support concurrent use either, doc/en/cam/CAM API Guide.md:38-39).  A wait gives up after a bound
 // (2 s), sets the status word and lets the launch end; the host reads it with step_status_read.
@@ -25,8 +29,13 @@
 
 namespace cam {
 
-// [0] route blocks done, [1] experts scanned, [2] dispatch waves past their wait, [3] status (1: a wait gave up)
-static __device__ __align__(256) int step_sync[64];
+// Counters, one per 128-byte line (SY_STRIDE ints): route shards, scan shards, dispatch-block shards, the top
+// counter of completed dispatch shards, the status word (1: a wait gave up)
+constexpr int SY_STRIDE = 32, SY_RSH = 8, SY_SSH = 8, SY_DSH = 64;
+constexpr int SY_ROUTED = 0, SY_SCANNED = SY_ROUTED + SY_RSH, SY_PASSED = SY_SCANNED + SY_SSH,
+              SY_TOP = SY_PASSED + SY_DSH, SY_STATUS = SY_TOP + 1, SY_SLOTS = SY_STATUS + 1;
+static __device__ __align__(256) int step_sync[SY_SLOTS * SY_STRIDE];
+__device__ __forceinline__ int *sy_slot(int *base, int i) { return base + i * SY_STRIDE; }
 
 struct StepArgs {
     const float *logits;
@@ -46,19 +55,24 @@ struct StepArgs {
     long long ticks;
 };
 
-// Waits until *ctr >= target (lane 0 polls, agent-coherent); false when the bound ran out (status set).
-__device__ __forceinline__ bool step_wait(int *ctr, int target, long long ticks, int *status, int sleep_units)
+// Waits until the n shards from slot `first` sum to at least target (lanes 0..n-1 poll, agent-coherent);
+// false when the bound ran out (status set).
+__device__ __forceinline__ bool step_wait(int *sync, int first, int n, int target, long long ticks, int sleep_units)
 {
+    const int lane = threadIdx.x & 63;
     const uint64_t t0 = wall_clock64();
     while (true) {
         int v = 0;
-        if ((threadIdx.x & 63) == 0)
-            v = __hip_atomic_load(gp(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < n)
+            v = __hip_atomic_load(gp(sy_slot(sync, first + lane)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1)
+            v += __shfl_xor(v, o, 64);
         if (__builtin_amdgcn_readfirstlane(v) >= target)
             return true;
         if ((long long)(wall_clock64() - t0) > ticks) {
-            if ((threadIdx.x & 63) == 0)
-                __hip_atomic_fetch_or(gp(status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)
+                __hip_atomic_fetch_or(gp(sy_slot(sync, SY_STATUS)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
         if (sleep_units >= 8)
@@ -71,46 +85,48 @@ __device__ __forceinline__ bool step_wait(int *ctr, int target, long long ticks,
 template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step_kernel(StepArgs a)
 {
     const int b = blockIdx.x;
-    int *routed = a.sync, *scanned = a.sync + 1, *passed = a.sync + 2, *status = a.sync + 3;
+    int *sync = a.sync;
+    auto bump = [&](int slot) {
+        return __hip_atomic_fetch_add(gp(sy_slot(sync, slot)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     if (b < a.nroute) {
         route_block<PER, true, true>(a.logits, a.bias, a.T, a.E, a.K, a.topk_idx, a.topk_w, nullptr, a.Ec, a.counts,
                                      a.pref, a.chunk_rank, b, a.nroute);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores have completed
         __syncthreads();                 // ... every wave's
         if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(gp(routed), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bump(SY_ROUTED + b % SY_RSH);
         return;
     }
     if (b < a.nroute + a.nscan) {
         const int e = (b - a.nroute) * 4 + (int)(threadIdx.x >> 6);
         if (e >= a.Ec)
             return;
-        step_wait(routed, a.nroute + a.extra, a.ticks, status, 2);
+        step_wait(sync, SY_ROUTED, SY_RSH, a.nroute + a.extra, a.ticks, 2);
         scan_expert<true>(e, a.nroute, a.counts, a.pref, a.send_offset, a.recv_count, a.tokens_per_expert);
         __builtin_amdgcn_s_waitcnt(0);
         if ((threadIdx.x & 63) == 0)
-            __hip_atomic_fetch_add(gp(scanned), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bump(SY_SCANNED + e % SY_SSH);
         return;
     }
-    const long item = (long)(b - a.nroute - a.nscan) * 4 + (threadIdx.x >> 6);
+    const int db = b - a.nroute - a.nscan, ndb = (a.ndisp_waves + 3) / 4;
+    const long item = (long)db * 4 + (threadIdx.x >> 6);
     const bool valid = item < (long)a.ndisp_waves;  // (only the last block can hold waves past the end)
-    // Wave 0 waits for the routing and the scan for the whole block (a few thousand resident waves polling one
-    // line would slow the stages they wait for), then the block meets.  Past the wait a wave reads no counter
-    // again: it counts itself, and the last one resets the counters.
+    // Wave 0 waits for the scan for the whole block (a few thousand resident waves polling would slow the stages
+    // they wait for), then the block meets.  Past the wait the block reads no counter again: wave 0 counts it in
+    // its shard; the block completing a shard bumps the top counter, the one completing that resets all.
     auto ready = [&]() {
         if (threadIdx.x < 64) {
-            if (step_wait(routed, a.nroute + a.extra, a.ticks, status, 8))
-                step_wait(scanned, a.Ec + a.extra, a.ticks, status, 8);
-        }
-        __syncthreads();
-        if (valid && (threadIdx.x & 63) == 0) {
-            const int n = __hip_atomic_fetch_add(gp(passed), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (n == a.ndisp_waves - 1) {
-                __hip_atomic_store(gp(routed), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(gp(scanned), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(gp(passed), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            step_wait(sync, SY_SCANNED, SY_SSH, a.Ec + a.extra, a.ticks, 8);
+            if (threadIdx.x == 0) {
+                const int sh = db % SY_DSH, in_shard = (ndb - sh + SY_DSH - 1) / SY_DSH;
+                if (bump(SY_PASSED + sh) == in_shard - 1 && bump(SY_TOP) == min(ndb, SY_DSH) - 1) {
+                    for (int i = 0; i < SY_STATUS; ++i)
+                        __hip_atomic_store(gp(sy_slot(sync, i)), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
+        __syncthreads();
     };
     if (!valid) {
         ready();  // meets the block's barrier
@@ -175,12 +191,12 @@ hipError_t step_status_read(int *status, bool clear)
     if (e != hipSuccess)
         return e;
     int v = 0;
-    e = hipMemcpy(&v, p + 3, sizeof(int), hipMemcpyDeviceToHost);
+    e = hipMemcpy(&v, p + SY_STATUS * SY_STRIDE, sizeof(int), hipMemcpyDeviceToHost);
     if (e != hipSuccess)
         return e;
     if (clear && v) {
         // a wait that gave up leaves the counters in an unknown state: start the next launch from zero
-        int zero[4] = {0, 0, 0, 0};
+        static const int zero[SY_SLOTS * SY_STRIDE] = {};
         e = hipMemcpy(p, zero, sizeof(zero), hipMemcpyHostToDevice);
         if (e != hipSuccess)
             return e;
