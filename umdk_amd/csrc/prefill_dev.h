@@ -268,11 +268,15 @@ struct RankSrc {
 };
 
 // Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
-template <bool CO>
+#ifndef CAM_STEP_COHERENT_DEST
+#define CAM_STEP_COHERENT_DEST 1
+#endif
+template <bool CO_>
 __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
                                              const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
                                              int T, int K, int E, int cap, int lane)
 {
+    constexpr bool CO = CO_ && CAM_STEP_COHERENT_DEST;
     int dst = -1;
     if (topk_idx == nullptr)  // identity mode (K = 1): row t of x quantised into row t
         return lane == 0 ? t : -1;

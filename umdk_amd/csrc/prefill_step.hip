@@ -19,6 +19,7 @@
 // when the library is loaded).  Launches that overlap on one GPU therefore race (the reference's prefill ops
 // do not support concurrent use either, doc/en/cam/CAM API Guide.md:38-39).  A wait gives up after a bound
 // (2 s), sets the status word and lets the launch end; the host reads it with step_status_read.
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <mutex>
@@ -37,6 +38,9 @@ constexpr int SY_ROUTED = 0, SY_SCANNED = SY_ROUTED + SY_RSH, SY_PASSED = SY_SCA
 static __device__ __align__(256) int step_sync[SY_SLOTS * SY_STRIDE];
 __device__ __forceinline__ int *sy_slot(int *base, int i) { return base + i * SY_STRIDE; }
 
+// dispatch blocks at most: about what the GPU holds at once (256 CUs x 8 blocks of 4 waves)
+constexpr int STEP_MAX_DISP_BLOCKS = 2048;
+
 struct StepArgs {
     const float *logits;
     const float *bias;
@@ -49,7 +53,7 @@ struct StepArgs {
     uint8_t *expand_x;
     float *scales;
     int32_t *expand_idx, *inv;
-    int nroute, nscan, ndisp_waves;
+    int nroute, nscan, ndisp_waves, ndisp_blocks;
     int extra;  // added to the wait targets: 1 makes every wait give up (a test hook)
     int *sync;
     long long ticks;
@@ -109,9 +113,9 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
             bump(SY_SCANNED + e % SY_SSH);
         return;
     }
-    const int db = b - a.nroute - a.nscan, ndb = (a.ndisp_waves + 3) / 4;
-    const long item = (long)db * 4 + (threadIdx.x >> 6);
-    const bool valid = item < (long)a.ndisp_waves;  // (only the last block can hold waves past the end)
+    // dispatch blocks loop over (token, chunk) items, item = i * 4 ndb + 4 db + wave: the wait, the count and the
+    // barrier happen once per block (every block paying a poll and an atomic round trip measured 76 vs 62 us)
+    const int db = b - a.nroute - a.nscan, ndb = a.ndisp_blocks;
     // Wave 0 waits for the scan for the whole block (a few thousand resident waves polling would slow the stages
     // they wait for), then the block meets.  Past the wait the block reads no counter again: wave 0 counts it in
     // its shard; the block completing a shard bumps the top counter, the one completing that resets all.
@@ -128,14 +132,20 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
         }
         __syncthreads();
     };
-    if (!valid) {
-        ready();  // meets the block's barrier
+    const RankSrc rs{nullptr, a.counts, a.chunk_rank, ROUTE_WAVES * 4};
+    long item = (long)db * 4 + (threadIdx.x >> 6);
+    if (item >= (long)a.ndisp_waves) {
+        ready();  // a wave without an item still meets the block's barrier
         return;
     }
-    const int t = (int)(item / a.nchunk), j = (int)(item % a.nchunk);
-    const RankSrc rs{nullptr, a.counts, a.chunk_rank, ROUTE_WAVES * 4};
-    dispatch_wave<MODE, true>(a.x, a.topk_idx, a.send_offset, rs, t, j, a.T, a.H, a.K, a.Ec, 0, a.cap, a.expand_x,
-                              a.scales, a.expand_idx, a.inv, a.kmajor, a.skip_unrouted, ready);
+    // the first item waits (after its loads of x are in flight), the others find the stages done
+    dispatch_wave<MODE, true>(a.x, a.topk_idx, a.send_offset, rs, (int)(item / a.nchunk), (int)(item % a.nchunk),
+                              a.T, a.H, a.K, a.Ec, 0, a.cap, a.expand_x, a.scales, a.expand_idx, a.inv, a.kmajor,
+                              a.skip_unrouted, ready);
+    for (item += 4l * ndb; item < (long)a.ndisp_waves; item += 4l * ndb)
+        dispatch_wave<MODE, true>(a.x, a.topk_idx, a.send_offset, rs, (int)(item / a.nchunk),
+                                  (int)(item % a.nchunk), a.T, a.H, a.K, a.Ec, 0, a.cap, a.expand_x, a.scales,
+                                  a.expand_idx, a.inv, a.kmajor, a.skip_unrouted, [] {});
 }
 
 // The array's device address on the current device, looked up once per device (host code never uses the
@@ -249,11 +259,12 @@ hipError_t launch_prefill_step(const float *logits, const float *bias, const uin
     a.nroute = (T + ROUTE_WAVES * 4 - 1) / (ROUTE_WAVES * 4);
     a.nscan = (Ec + 3) / 4;
     a.ndisp_waves = T * a.nchunk;
+    a.ndisp_blocks = std::min((a.ndisp_waves + 3) / 4, STEP_MAX_DISP_BLOCKS);
     a.sync = sync;
     a.extra = g_step_unreach.load(std::memory_order_relaxed);
     const long long tk = g_step_ticks.load(std::memory_order_relaxed);
     a.ticks = tk > 0 ? tk : 200000000LL;  // 2 s of the 100 MHz constant clock
-    const unsigned grid = (unsigned)(a.nroute + a.nscan + (a.ndisp_waves + 3) / 4);
+    const unsigned grid = (unsigned)(a.nroute + a.nscan + a.ndisp_blocks);
     const int per = (E + 15) >> 4;
 #define STEP_CASE(P)                                                                                                \
     do {                                                                                                            \
