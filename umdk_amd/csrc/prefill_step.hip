@@ -34,7 +34,8 @@ namespace cam {
 // counter of completed dispatch shards, the status word (1: a wait gave up)
 constexpr int SY_STRIDE = 32, SY_RSH = 8, SY_SSH = 8, SY_DSH = 64;
 constexpr int SY_ROUTED = 0, SY_SCANNED = SY_ROUTED + SY_RSH, SY_PASSED = SY_SCANNED + SY_SSH,
-              SY_TOP = SY_PASSED + SY_DSH, SY_STATUS = SY_TOP + 1, SY_SLOTS = SY_STATUS + 1;
+              SY_TOP = SY_PASSED + SY_DSH, SY_RTOP = SY_TOP + 1, SY_STOP = SY_RTOP + 1, SY_RDONE = SY_STOP + 1,
+              SY_SDONE = SY_RDONE + 1, SY_STATUS = SY_SDONE + 1, SY_SLOTS = SY_STATUS + 1;
 static __device__ __align__(256) int step_sync[SY_SLOTS * SY_STRIDE];
 __device__ __forceinline__ int *sy_slot(int *base, int i) { return base + i * SY_STRIDE; }
 
@@ -59,19 +60,18 @@ struct StepArgs {
     long long ticks;
 };
 
-// Waits until the n shards from slot `first` sum to at least target (lanes 0..n-1 poll, agent-coherent);
-// false when the bound ran out (status set).
-__device__ __forceinline__ bool step_wait(int *sync, int first, int n, int target, long long ticks, int sleep_units)
+// Waits until the flag in `slot` reaches target (lane 0 polls, agent-coherent, a long sleep between polls:
+// coherent reads of one line are served one at a time at the memory side, and thousands of waves polling it
+// slow down the very stages they wait for); false when the bound ran out (status set).
+template <int SLEEP>
+__device__ __forceinline__ bool step_wait(int *sync, int slot, int target, long long ticks)
 {
     const int lane = threadIdx.x & 63;
     const uint64_t t0 = wall_clock64();
     while (true) {
         int v = 0;
-        if (lane < n)
-            v = __hip_atomic_load(gp(sy_slot(sync, first + lane)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1)
-            v += __shfl_xor(v, o, 64);
+        if (lane == 0)
+            v = __hip_atomic_load(gp(sy_slot(sync, slot)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane(v) >= target)
             return true;
         if ((long long)(wall_clock64() - t0) > ticks) {
@@ -79,10 +79,7 @@ __device__ __forceinline__ bool step_wait(int *sync, int first, int n, int targe
                 __hip_atomic_fetch_or(gp(sy_slot(sync, SY_STATUS)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
-        if (sleep_units >= 8)
-            __builtin_amdgcn_s_sleep(8);
-        else
-            __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(SLEEP);
     }
 }
 
@@ -93,24 +90,34 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
     auto bump = [&](int slot) {
         return __hip_atomic_fetch_add(gp(sy_slot(sync, slot)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
+    // counts one of `total` items in shard i of `nsh` (items i, i + nsh, ...); the item completing a shard bumps
+    // `top`, the one completing `top` raises `done` (so waiters read one flag)
+    auto count = [&](int shard_base, int nsh, int i, int total, int top, int done) {
+        const int sh = i % nsh, in_shard = (total - sh + nsh - 1) / nsh;
+        if (bump(shard_base + sh) == in_shard - 1 && bump(top) == min(total, nsh) - 1)
+            __hip_atomic_store(gp(sy_slot(sync, done)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     if (b < a.nroute) {
         route_block<PER, true, true>(a.logits, a.bias, a.T, a.E, a.K, a.topk_idx, a.topk_w, nullptr, a.Ec, a.counts,
                                      a.pref, a.chunk_rank, b, a.nroute);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores have completed
         __syncthreads();                 // ... every wave's
         if (threadIdx.x == 0)
-            bump(SY_ROUTED + b % SY_RSH);
+            count(SY_ROUTED, SY_RSH, b, a.nroute, SY_RTOP, SY_RDONE);
         return;
     }
     if (b < a.nroute + a.nscan) {
         const int e = (b - a.nroute) * 4 + (int)(threadIdx.x >> 6);
+#if defined(CAM_STEP_PHASES) && CAM_STEP_PHASES == 1
+        return;
+#endif
         if (e >= a.Ec)
             return;
-        step_wait(sync, SY_ROUTED, SY_RSH, a.nroute + a.extra, a.ticks, 2);
+        step_wait<16>(sync, SY_RDONE, 1 + a.extra, a.ticks);
         scan_expert<true>(e, a.nroute, a.counts, a.pref, a.send_offset, a.recv_count, a.tokens_per_expert);
         __builtin_amdgcn_s_waitcnt(0);
         if ((threadIdx.x & 63) == 0)
-            bump(SY_SCANNED + e % SY_SSH);
+            count(SY_SCANNED, SY_SSH, e, a.Ec, SY_STOP, SY_SDONE);
         return;
     }
     // dispatch blocks loop over (token, chunk) items, item = i * 4 ndb + 4 db + wave: the wait, the count and the
@@ -121,7 +128,7 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
     // its shard; the block completing a shard bumps the top counter, the one completing that resets all.
     auto ready = [&]() {
         if (threadIdx.x < 64) {
-            step_wait(sync, SY_SCANNED, SY_SSH, a.Ec + a.extra, a.ticks, 8);
+            step_wait<64>(sync, SY_SDONE, 1 + a.extra, a.ticks);
             if (threadIdx.x == 0) {
                 const int sh = db % SY_DSH, in_shard = (ndb - sh + SY_DSH - 1) / SY_DSH;
                 if (bump(SY_PASSED + sh) == in_shard - 1 && bump(SY_TOP) == min(ndb, SY_DSH) - 1) {
@@ -134,6 +141,10 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
     };
     const RankSrc rs{nullptr, a.counts, a.chunk_rank, ROUTE_WAVES * 4};
     long item = (long)db * 4 + (threadIdx.x >> 6);
+#ifdef CAM_STEP_PHASES  // diagnostic variants: routing and scan (and the dispatch blocks' wait), no dispatch
+    ready();
+    return;
+#endif
     if (item >= (long)a.ndisp_waves) {
         ready();  // a wave without an item still meets the block's barrier
         return;
