@@ -430,7 +430,7 @@ camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(const float *logits, const
             int32_t *chunk_rank = (int32_t *)((uint8_t *)w + rank_off);
             // bf16 and fp8 rows: the three stages in one launch (prefill_step.hip); int8 (whose per-token scale
             // needs a whole row per wave) in three
-            if (q != CAMHIP_QUANT_INT8_TOKEN && cam::step_fused_enabled())
+            if (q != CAMHIP_QUANT_INT8_TOKEN && cam::step_fused_mode() != 0)
                 return cam::launch_prefill_step(logits, bias, x, T, H, E, L, K, q, cap, kmajor, L < E, topkIdx,
                                                 topkWeights, counts, pref, chunk_rank, send_off, recvCount,
                                                 recvTokensPerExpert, recvX, recvXScales, expandIdx, combineRowMap, s);

@@ -41,7 +41,7 @@ hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pre
 // bf16 / fp8 dispatch in one launch (prefill_step.hip): the outputs of launch_route_hist + launch_scan_notify +
 // launch_dispatch(chunk_base = counts, chunk_rank, skip_unrouted); counts/pref/chunk_rank/send_offset are the
 // same workspace arrays.  Launches that overlap on one GPU race (a static per-device set of counters).
-bool step_fused_enabled();
+int step_fused_mode();  // 0: three launches, 1: routing + scan in one, then the dispatch, 2: one launch
 hipError_t launch_prefill_step(const float *logits, const float *bias, const uint16_t *x, int T, int H, int E, int Ec,
                                int K, int quant_mode, int cap, bool kmajor, bool skip_unrouted, int32_t *topk_idx,
                                float *topk_w, int32_t *counts, int32_t *pref, int32_t *chunk_rank,

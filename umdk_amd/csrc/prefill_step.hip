@@ -41,6 +41,7 @@ __device__ __forceinline__ int *sy_slot(int *base, int i) { return base + i * SY
 
 // dispatch blocks at most: about what the GPU holds at once (256 CUs x 8 blocks of 4 waves)
 constexpr int STEP_MAX_DISP_BLOCKS = 2048;
+constexpr int STEP_DEFAULT_MODE = 1;
 
 struct StepArgs {
     const float *logits;
@@ -116,8 +117,19 @@ template <int PER, int MODE> __global__ __launch_bounds__(256) void prefill_step
         step_wait<16>(sync, SY_RDONE, 1 + a.extra, a.ticks);
         scan_expert<true>(e, a.nroute, a.counts, a.pref, a.send_offset, a.recv_count, a.tokens_per_expert);
         __builtin_amdgcn_s_waitcnt(0);
-        if ((threadIdx.x & 63) == 0)
-            count(SY_SCANNED, SY_SSH, e, a.Ec, SY_STOP, SY_SDONE);
+        if ((threadIdx.x & 63) == 0) {
+            if (a.ndisp_blocks > 0) {
+                count(SY_SCANNED, SY_SSH, e, a.Ec, SY_STOP, SY_SDONE);
+            } else {
+                // routing + scan only (the dispatch is a launch of its own): the wave completing the scan
+                // resets the counters -- every scan wave has read the routing flag by then
+                const int sh = e % SY_SSH, in_shard = (a.Ec - sh + SY_SSH - 1) / SY_SSH;
+                if (bump(SY_SCANNED + sh) == in_shard - 1 && bump(SY_STOP) == min(a.Ec, SY_SSH) - 1) {
+                    for (int i = 0; i < SY_STATUS; ++i)
+                        __hip_atomic_store(gp(sy_slot(sync, i)), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
         return;
     }
     // dispatch blocks loop over (token, chunk) items, item = i * 4 ndb + 4 db + wave: the wait, the count and the
@@ -187,14 +199,15 @@ static hipError_t step_sync_ptr(int **out)
     return hipSuccess;
 }
 
-// CAMHIP_STEP_FUSED=0 in the environment selects the three-launch step (for measuring one against the other)
-bool step_fused_enabled()
+// CAMHIP_STEP_FUSED in the environment (for measuring the forms against each other): 0 -- three launches,
+// 1 -- routing + scan in one launch, then the dispatch, 2 -- all three stages in one launch
+int step_fused_mode()
 {
-    static const bool on = [] {
+    static const int mode = [] {
         const char *v = getenv("CAMHIP_STEP_FUSED");
-        return !(v && v[0] == '0');
+        return v && v[0] >= '0' && v[0] <= '2' ? v[0] - '0' : STEP_DEFAULT_MODE;
     }();
-    return on;
+    return mode;
 }
 
 static std::atomic<long long> g_step_ticks{0};
@@ -270,7 +283,8 @@ hipError_t launch_prefill_step(const float *logits, const float *bias, const uin
     a.nroute = (T + ROUTE_WAVES * 4 - 1) / (ROUTE_WAVES * 4);
     a.nscan = (Ec + 3) / 4;
     a.ndisp_waves = T * a.nchunk;
-    a.ndisp_blocks = std::min((a.ndisp_waves + 3) / 4, STEP_MAX_DISP_BLOCKS);
+    const bool all_in_one = step_fused_mode() == 2;
+    a.ndisp_blocks = all_in_one ? std::min((a.ndisp_waves + 3) / 4, STEP_MAX_DISP_BLOCKS) : 0;
     a.sync = sync;
     a.extra = g_step_unreach.load(std::memory_order_relaxed);
     const long long tk = g_step_ticks.load(std::memory_order_relaxed);
@@ -297,7 +311,11 @@ hipError_t launch_prefill_step(const float *logits, const float *bias, const uin
     else
         STEP_CASE(32);
 #undef STEP_CASE
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess || all_in_one)
+        return e;
+    return launch_dispatch(x, topk_idx, send_offset, nullptr, T, H, K, Ec, 0, cap, quant_mode, expand_x, scales,
+                           expand_idx, s, inv, nullptr, kmajor, counts, ROUTE_WAVES * 4, chunk_rank, skip_unrouted);
 }
 
 }  // namespace cam
