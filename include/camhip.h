@@ -169,11 +169,7 @@ CAMHIP_API camhipStatus camhipMoeCombineNormal(void *workspace, uint64_t workspa
  *   0..localExperts-1 (other ids are not routed on this rank), the layout, count exchange and
  *   camhipMoeDispatchNormal.  The per-expert rank of each (t,k) is not materialised (send_token_idx): the
  *   routing writes per-chunk expert histograms, a scan turns them into chunk bases and runs the count
- *   exchange, and the dispatch ranks each entry inside its chunk.  For bf16 and fp8 rows the three stages run
- *   as one launch whose blocks wait on each other through a static per-device set of counters: calls that
- *   overlap on one GPU must be serialised by the caller (as for the reference's prefill ops, "does not
- *   support concurrent usage"); a wait that gives up is reported by camhipGetSyncStatus.  int8 rows: three
- *   launches.  Outputs: topkIdx/topkWeights [numTokens, topK],
+ *   exchange, and the dispatch ranks each entry inside its chunk (three launches).  Outputs: topkIdx/topkWeights [numTokens, topK],
  *   recvX and recvXScales as the dispatch call's quantMode (0, 2, 3, 5), expandIdx [rows, 3], recvCount
  *   [localExperts] (inclusive prefix), recvTokensPerExpert [localExperts] int64, and combineRowMap
  *   [numTokens, topK] = the row of (t,k), or -1, which replaces the combine's own scatter pass.
@@ -302,12 +298,11 @@ CAMHIP_API camhipStatus camhipMoeExpertsGetWorkspaceSize(const void *x, const fl
 CAMHIP_API camhipStatus camhipMoeExperts(void *workspace, uint64_t workspaceSize, camhipExecutor *executor,
                                          void *stream);
 
-/* Sync status of the current device's launches that wait on other blocks of the same launch (extension, no
- * reference counterpart): bit 0 -- a readiness wait of a chained GEMM launch (camhipMoeExperts,
- * camhipFusedDeepMoe) gave up; bit 1 -- a wait of the single-launch prefill dispatch step
- * (camhipMoePrefillDispatch) gave up.  Sticky; clear != 0 resets both (and the step's counters).  A wait only
- * gives up when blocks of its launch cannot run (a GPU shared with other work that holds the compute units);
- * the launch's outputs are then unspecified.  Synchronous: call it after the launches have completed. */
+/* Sync status of the current device's chained GEMM launches (camhipMoeExperts, camhipFusedDeepMoe), an
+ * extension with no reference counterpart: *status = 0, or nonzero once a readiness wait gave up (sticky;
+ * clear != 0 resets it).  A wait only gives up when blocks of its launch cannot run (a GPU shared with other
+ * work that holds the compute units); the launch's outputs are then unspecified.  Synchronous: call it after
+ * the launches have completed. */
 CAMHIP_API camhipStatus camhipGetSyncStatus(int32_t *status, int32_t clear);
 /* Test hook (extension): waitTicks > 0 sets the chained launches' wait bound in 100 MHz constant-clock
  * ticks (<= 0 restores 2 s); unreachable != 0 makes every wait unreachable, so that each one gives up at

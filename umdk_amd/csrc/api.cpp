@@ -428,12 +428,6 @@ camhipStatus camhipMoePrefillDispatchGetWorkspaceSize(const float *logits, const
             int32_t *pref = (int32_t *)((uint8_t *)w + counts_bytes);
             int32_t *send_off = (int32_t *)((uint8_t *)w + 2 * counts_bytes);
             int32_t *chunk_rank = (int32_t *)((uint8_t *)w + rank_off);
-            // bf16 and fp8 rows: the three stages in one launch (prefill_step.hip); int8 (whose per-token scale
-            // needs a whole row per wave) in three
-            if (q != CAMHIP_QUANT_INT8_TOKEN && cam::step_fused_mode() != 0)
-                return cam::launch_prefill_step(logits, bias, x, T, H, E, L, K, q, cap, kmajor, L < E, topkIdx,
-                                                topkWeights, counts, pref, chunk_rank, send_off, recvCount,
-                                                recvTokensPerExpert, recvX, recvXScales, expandIdx, combineRowMap, s);
             hipError_t e = cam::launch_route_hist(logits, bias, T, E, K, L, topkIdx, topkWeights, counts, pref,
                                                   chunk_rank, s);
             if (e != hipSuccess)
@@ -707,13 +701,11 @@ camhipStatus camhipMoeExperts(void *workspace, uint64_t workspaceSize, camhipExe
 camhipStatus camhipGetSyncStatus(int32_t *status, int32_t clear)
 {
     CHECK_PTR(status);
-    int v = 0, v2 = 0;
+    int v = 0;
     hipError_t e = cam::sync_status_read(&v, clear != 0);
-    if (e == hipSuccess)
-        e = cam::step_status_read(&v2, clear != 0);
     if (e != hipSuccess)
         return fail(CAMHIP_ERROR_RUNTIME, "get_sync_status: %s", hipGetErrorString(e));
-    *status = v | (v2 << 1);
+    *status = v;
     g_last_error.clear();
     return CAMHIP_SUCCESS;
 }
@@ -721,7 +713,6 @@ camhipStatus camhipGetSyncStatus(int32_t *status, int32_t clear)
 void camhipDebugSetSyncWait(int64_t waitTicks, int32_t unreachable)
 {
     cam::sync_debug_set(waitTicks, unreachable);
-    cam::step_debug_set(waitTicks, unreachable);
 }
 
 }  // extern "C"

@@ -37,19 +37,6 @@ hipError_t launch_layout(const int64_t *topk_idx, int T, int K, int E, int R, in
 // the row totals and the summed chunk prefixes [E][nc] of launch_route_hist
 hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pref, int32_t *send_offset,
                               int32_t *recv_count, int64_t *tokens_per_expert, hipStream_t s);
-// the prefill step's routing (over E experts), chunk scan + count exchange (over the Ec local experts) and
-// bf16 / fp8 dispatch in one launch (prefill_step.hip): the outputs of launch_route_hist + launch_scan_notify +
-// launch_dispatch(chunk_base = counts, chunk_rank, skip_unrouted); counts/pref/chunk_rank/send_offset are the
-// same workspace arrays.  Launches that overlap on one GPU race (a static per-device set of counters).
-int step_fused_mode();  // 0: three launches, 1: routing + scan in one, then the dispatch, 2: one launch
-hipError_t launch_prefill_step(const float *logits, const float *bias, const uint16_t *x, int T, int H, int E, int Ec,
-                               int K, int quant_mode, int cap, bool kmajor, bool skip_unrouted, int32_t *topk_idx,
-                               float *topk_w, int32_t *counts, int32_t *pref, int32_t *chunk_rank,
-                               int32_t *send_offset, int32_t *recv_count, int64_t *tokens_per_expert,
-                               void *expand_x, float *scales, int32_t *expand_idx, int32_t *inv, hipStream_t s);
-// its status word (nonzero: a wait gave up; clear also zeroes the counters) and the test hooks of its waits
-hipError_t step_status_read(int *status, bool clear);
-void step_debug_set(long long wait_ticks, int unreachable);
 // int32 topk ids, used by the fused path
 hipError_t launch_layout_i32(const int32_t *topk_idx, int T, int K, int E, int32_t *ntok_per_expert,
                              int32_t *send_token_idx, void *ws, hipStream_t s);

@@ -1,10 +1,12 @@
 // Device bodies of the prefill step's three stages -- routing of a 16-token chunk (R0 + the chunk histograms
-// of D1), one expert's chunk scan and count exchange (D1 + D2), one dispatch wave (D3 + Q1) -- shared by their
-// separate kernels (route.hip, layout.hip, dispatch.hip) and by the single-launch step (prefill_step.hip).
+// of D1), one expert's chunk scan and count exchange (D1 + D2), one dispatch wave (D3 + Q1) -- used by their
+// kernels (route.hip, layout.hip, dispatch.hip).
 //
-// CO (coherent): the single-launch step runs the stages in one grid, so a stage's outputs that a later stage
-// reads inside the launch are stored agent-coherently (written through to memory) and read the same way: the
-// reading wave may sit on another XCD, whose L2 the writer's stores do not reach.
+// CO (coherent): for a kernel that runs two stages in one grid, a stage's outputs that a later stage reads
+// inside the launch are stored agent-coherently (written through to memory) and read the same way, since the
+// reading wave may sit on another XCD, whose L2 the writer's stores do not reach.  (Measured: the routing,
+// scan and dispatch in one launch, stages waiting on each other through counters, 65-67 us against 62-63 us
+// for three launches at config 2's shape; a kernel boundary gives the same ordering for less.)
 #pragma once
 #include "cam_device.h"
 
@@ -268,15 +270,11 @@ struct RankSrc {
 };
 
 // Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
-#ifndef CAM_STEP_COHERENT_DEST
-#define CAM_STEP_COHERENT_DEST 1
-#endif
-template <bool CO_>
+template <bool CO>
 __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
                                              const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
                                              int T, int K, int E, int cap, int lane)
 {
-    constexpr bool CO = CO_ && CAM_STEP_COHERENT_DEST;
     int dst = -1;
     if (topk_idx == nullptr)  // identity mode (K = 1): row t of x quantised into row t
         return lane == 0 ? t : -1;
@@ -303,8 +301,8 @@ __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_id
 // (MODE 3: amax clamped to >= 1e-4, q = e4m3_rne_sat(x * (448/amax)), scale = amax/448; a 128-block is 8
 // adjacent lanes, so its amax is a 3-step xor shuffle).  The slice of x is read once (16-byte loads),
 // quantised once in registers and written to each of the token's K destination rows with 16-byte stores.
-// `ready()` is called between the loads of x and the first read of the routing results (the single-launch
-// step waits there for the routing and the scan; a no-op otherwise).  skip_unrouted: a token none of whose
+// `ready()` is called between the loads of x and the first read of the routing results (a hook for a kernel
+// that waits there for earlier stages of the same launch; a no-op in the dispatch kernel).  skip_unrouted: a token none of whose
 // picks is below E reads nothing and only writes its row-map entries (`ready()` comes first then).
 template <int MODE, bool CO, typename Ready>
 __device__ __forceinline__ void dispatch_wave(const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx,
