@@ -4,10 +4,11 @@
 //   prepare ids (x_active_mask, local expert range) -> layout -> count
 //   exchange -> quantised dispatch -> GMM1+SwiGLU -> GMM2 -> combine,
 //   plus the optional shared expert on all tokens.  At decode sizes
-//   (batch*topk <= 8192) the first three stages are one single-block launch,
-//   dispatch writes the combine's row map, and GMM1 and GMM2 run as one
-//   chained launch (fp8, bf16; each GMM2 tile waits for the GMM1 tiles of its
-//   rows): four launches in all.
+//   (batch*topk <= 2048, bf16 or fp8) the first four stages are one launch
+//   (every block computes the layout in LDS), dispatch writes the combine's
+//   row map, and GMM1 and GMM2 run as one chained launch (each GMM2 tile waits
+//   for the GMM1 tiles of its rows): three launches in all.  int8 and
+//   batch*topk <= 8192: the first three stages are one single-block launch.
 // Every intermediate lives in the caller's workspace and every size is fixed
 // by (batch, topk): no host synchronisation and no allocation, so the call can
 // be captured in a HIP graph (the reference's fused op is its graph-capturable
@@ -233,7 +234,14 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         const bool chained = cam::gmm_chain_supported(g1, g2, dt);
         int32_t *ready = (int32_t *)P(f.ready);
         const int nready = chained ? cam::gmm_chain_counters(N, L) : 0;
-        if (N <= 8192) {
+        // decode sizes with bf16 or fp8 rows: id preparation, layout, count exchange and the dispatch in one
+        // launch (which also clears the counters)
+        const bool one_launch = !int8 && cam::dispatch_decode_fits(T, K, L);
+        if (one_launch) {
+            HIP_TRY(cam::launch_dispatch_decode(expertIds, xActiveMask, x, T, H, K, L, N, q, P(f.ex), (float *)P(f.xs),
+                                                (int32_t *)P(f.eidx), (int32_t *)P(f.inv), true, counts, send_off,
+                                                recv_cnt, (int32_t *)P(f.total), expertTokenNums, s, ready, nready));
+        } else if (N <= 8192) {
             // decode sizes: id preparation, layout and count exchange in one launch (which also clears the
             // counters)
             HIP_TRY(cam::launch_layout_small(expertIds, xActiveMask, T, K, L, ids, counts, (int32_t *)P(f.sti),
@@ -249,9 +257,10 @@ camhipStatus camhipFusedDeepMoeGetWorkspaceSize(
         }
         // dispatch also writes the combine's row map (inv), so the combine is a single gather; fp8 block
         // scales come out k-major, the layout GMM1 reads
-        HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
-                                     (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv),
-                                     expertSmoothScales, true));
+        if (!one_launch)
+            HIP_TRY(cam::launch_dispatch(x, ids, send_off, (int32_t *)P(f.sti), T, H, K, L, 0, N, q, P(f.ex),
+                                         (float *)P(f.xs), (int32_t *)P(f.eidx), s, (int32_t *)P(f.inv),
+                                         expertSmoothScales, true));
         if (chained) {
             HIP_TRY(cam::launch_gmm_chain(g1, g2, dt, ready, s));
         } else {

@@ -63,6 +63,15 @@ hipError_t launch_dispatch(const uint16_t *x, const int32_t *topk_idx, const int
                            int32_t *inv_out = nullptr, const float *smooth = nullptr, bool kmajor_scales = false,
                            const int32_t *chunk_base = nullptr, int tpc = 0, const int32_t *chunk_rank = nullptr,
                            bool skip_unrouted = false);
+// decode sizes (dispatch_decode_fits: T*K <= 2048, E <= 512; bf16 or fp8 rows): layout + count exchange +
+// dispatch as one launch (the arguments of launch_layout_small and launch_dispatch; the ranks and effective ids
+// stay in LDS)
+hipError_t launch_dispatch_decode(const int32_t *ids, const uint8_t *active, const uint16_t *x, int T, int H, int K,
+                                  int E, int cap, int quant_mode, void *expand_x, float *scales, int32_t *expand_idx,
+                                  int32_t *inv_out, bool kmajor_scales, int32_t *counts, int32_t *send_offset,
+                                  int32_t *recv_count, int32_t *total, int64_t *tokens_per_expert, hipStream_t s,
+                                  int32_t *zero, int nzero);
+bool dispatch_decode_fits(int T, int K, int E);
 // (send_token_idx == nullptr: the rank within the expert is chunk_base[e * nc + t / tpc] plus chunk_rank[t * K + k],
 // the rank inside the token's chunk of tpc tokens; skip_unrouted: tokens with no pick in [0, E) read nothing, for a
 // rank that holds only some of the experts)
