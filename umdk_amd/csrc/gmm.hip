@@ -1776,7 +1776,9 @@ hipError_t sync_status_read(int *status, bool clear)
 template <int DT, int EPI1> static hipError_t launch_chain_t(GmmArgs g1, GmmArgs g2, GmmSync sy, hipStream_t s)
 {
     const int dev = current_device();
-    const int grid = (num_cus(dev) + 7) / 8 * 8;
+    // one block per CU at most (a block's GMM2 tiles wait for GMM1 tiles of other blocks, so every block must be
+    // resident at once), in whole XCD rounds where the CU count allows
+    const int cus = num_cus(dev), grid = cus >= 8 ? cus / 8 * 8 : cus;
     if (chain_small(g1)) {
         static std::atomic<bool> done[G_MAX_DEVICES];
         hipError_t e = set_lds(gmm_chain_small<DT, EPI1>, G_LDS_SMALL_BYTES, dev, done);
