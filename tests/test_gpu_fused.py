@@ -98,8 +98,10 @@ def chain_small_ops(ops, d, E, K):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-# the last case (1100 x 8 > 8192 entries) takes the prefill-sized bookkeeping path
+# up to 2048 (token, k) entries the layout runs inside the dispatch launch (256 x 8: the limit; 512 experts);
+# 300 x 8 takes the single-block layout launch, 1100 x 8 > 8192 entries the prefill-sized bookkeeping path
 @pytest.mark.parametrize("bs,H,I,E,K", [(16, 7168, 1024, 16, 8), (128, 2048, 512, 32, 8), (3, 1024, 128, 8, 2),
+                                        (256, 1024, 128, 16, 8), (64, 1024, 128, 512, 8), (300, 1024, 128, 16, 8),
                                         (1100, 1024, 128, 16, 8)])
 def test_fused_equals_small_op_chain(ops, dtype, bs, H, I, E, K):
     print(f"fused vs chain {dtype} bs={bs} H={H} I={I} E={E} K={K}", flush=True)
