@@ -40,8 +40,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_chunk_kernel(
     if (item >= (long)T * nchunk)
         return;
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
-    dispatch_wave<MODE, false>(x, topk_idx, send_offset, rs, t, j, T, H, K, E, rank, cap, expand_x, scales,
-                               expand_idx, inv_out, kmajor, skip_unrouted, [] {});
+    dispatch_wave<MODE>(x, topk_idx, send_offset, rs, t, j, T, H, K, E, rank, cap, expand_x, scales, expand_idx,
+                        inv_out, kmajor, skip_unrouted, [] {});
 }
 
 // int8 per-token quantisation needs the whole row's amax: one wave per token,
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
     const int t = blockIdx.x * DISP_WAVES + (threadIdx.x >> 6);
     if (t >= T)
         return;
-    const int dst = dispatch_dest<false>(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+    const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
     if (inv_out && lane < K)
         inv_out[(size_t)t * K + lane] = dst;
     const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + (size_t)t * H);
@@ -271,8 +271,8 @@ __global__ __launch_bounds__(DEC_THREADS) void dispatch_decode_kernel(
     }
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
     const RankSrc rs{s_rank, nullptr, nullptr, 0};
-    dispatch_wave<MODE, false>(x, s_ids, s_off, rs, t, j, T, H, K, E, 0, cap, expand_x, scales, expand_idx, inv_out,
-                               kmajor, 0, layout);
+    dispatch_wave<MODE>(x, s_ids, s_off, rs, t, j, T, H, K, E, 0, cap, expand_x, scales, expand_idx, inv_out,
+                        kmajor, 0, layout);
 }
 
 hipError_t launch_dispatch_decode(const int32_t *ids, const uint8_t *active, const uint16_t *x, int T, int H, int K,

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(SN_THREADS) void scan_notify_kernel(int E, int nc, 
     const int e = blockIdx.x * SN_WAVES + (int)(threadIdx.x >> 6);
     if (e >= E)
         return;
-    scan_expert<false>(e, nc, counts, pref, send_offset, recv_count, tokens_per_expert);
+    scan_expert(e, nc, counts, pref, send_offset, recv_count, tokens_per_expert);
 }
 
 hipError_t launch_scan_notify(int E, int nc, int32_t *counts, const int32_t *pref, int32_t *send_offset,

@@ -1,39 +1,12 @@
 // Device bodies of the prefill step's three stages -- routing of a 16-token chunk (R0 + the chunk histograms
 // of D1), one expert's chunk scan and count exchange (D1 + D2), one dispatch wave (D3 + Q1) -- used by their
-// kernels (route.hip, layout.hip, dispatch.hip).
-//
-// CO (coherent): for a kernel that runs two stages in one grid, a stage's outputs that a later stage reads
-// inside the launch are stored agent-coherently (written through to memory) and read the same way, since the
-// reading wave may sit on another XCD, whose L2 the writer's stores do not reach.  (Measured: the routing,
-// scan and dispatch in one launch, stages waiting on each other through counters, 65-67 us against 62-63 us
-// for three launches at config 2's shape; a kernel boundary gives the same ordering for less.)
+// kernels (route.hip, layout.hip, dispatch.hip).  (Measured: the three stages in one launch, waiting on each
+// other through counters, took 65-67 us against 62-63 us for three launches at config 2's shape; a kernel
+// boundary gives the same ordering for less.)
 #pragma once
 #include "cam_device.h"
 
 namespace cam {
-
-// ---------------------------------------------------------------- coherent access
-template <typename T> __device__ __forceinline__ __attribute__((address_space(1))) T *gp(T *p)
-{
-    return (__attribute__((address_space(1))) T *)p;
-}
-template <typename T> struct co_ident {
-    using type = T;
-};
-template <bool CO, typename T> __device__ __forceinline__ void co_st(T *p, typename co_ident<T>::type v)
-{
-    if constexpr (CO)
-        __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-        *p = v;
-}
-template <bool CO, typename T> __device__ __forceinline__ T co_ld(const T *p)
-{
-    if constexpr (CO)
-        return __hip_atomic_load(gp(const_cast<T *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-        return *p;
-}
 
 // ---------------------------------------------------------------- R0: routing
 // A token is handled by a 16-lane row of a wave (four tokens per wave); lane l of the row holds experts l,
@@ -76,7 +49,7 @@ __device__ __forceinline__ uint32_t order_key(float s)
 // earlier tokens of the chunk that picked the expert: each expert gets a 16-bit mask of the chunk's tokens that
 // picked it (an LDS atomic OR, which no order of the ORs changes), the rank is the popcount of the mask below
 // the token, the count that of the whole mask.
-template <int PER, bool HIST, bool CO>
+template <int PER, bool HIST>
 __device__ __forceinline__ void route_block(const float *__restrict__ logits, const float *__restrict__ bias, int T,
                                             int E, int K, int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
                                             int64_t *__restrict__ topk_idx64, int Ec, int32_t *__restrict__ chunk_counts,
@@ -148,7 +121,7 @@ __device__ __forceinline__ void route_block(const float *__restrict__ logits, co
     for (int k = 0; k < K; ++k)
         denom += __shfl(my_ex, (lane & 48) | k, 64);
     if (l16 < K && live) {
-        co_st<CO>(topk_idx + (size_t)t * K + l16, my_idx);
+        topk_idx[(size_t)t * K + l16] = my_idx;
         topk_w[(size_t)t * K + l16] = my_ex / denom;
         if (topk_idx64)
             topk_idx64[(size_t)t * K + l16] = my_idx;
@@ -165,7 +138,7 @@ __device__ __forceinline__ void route_block(const float *__restrict__ logits, co
             atomicOr(&picked[my_idx], 1u << tl);
         __syncthreads();
         if (local)
-            co_st<CO>(chunk_rank + (size_t)t * K + l16, __popc(picked[my_idx] & ((1u << tl) - 1u)));
+            chunk_rank[(size_t)t * K + l16] = __popc(picked[my_idx] & ((1u << tl) - 1u));
         // the histogram, and its exclusive prefix over the experts: thread i owns experts [i PE, (i + 1) PE)
         constexpr int NT = ROUTE_WAVES * 64, PE = (ROUTE_MAX_PER_LANE * 16 + NT - 1) / NT;
         __shared__ int32_t wsum[ROUTE_WAVES];
@@ -193,8 +166,8 @@ __device__ __forceinline__ void route_block(const float *__restrict__ logits, co
         for (int q = 0; q < PE; ++q) {
             const int e = threadIdx.x * PE + q;
             if (e < Ec) {
-                co_st<CO>(chunk_counts + (size_t)e * nb + b, cnt[q]);
-                co_st<CO>(chunk_pref + (size_t)e * nb + b, run);
+                chunk_counts[(size_t)e * nb + b] = cnt[q];
+                chunk_pref[(size_t)e * nb + b] = run;
             }
             run += cnt[q];
         }
@@ -206,7 +179,6 @@ __device__ __forceinline__ void route_block(const float *__restrict__ logits, co
 // its row of chunk prefixes (each chunk's count of the lower experts' picks) into its send offset, so every
 // expert's count exchange entry is known without a second pass over the totals: send_offset = exclusive,
 // recv_count = inclusive prefix over the experts, tokens_per_expert as int64.
-template <bool CO>
 __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__ counts,
                                             const int32_t *__restrict__ pref, int32_t *__restrict__ send_offset,
                                             int32_t *__restrict__ recv_count, int64_t *__restrict__ tokens_per_expert)
@@ -218,8 +190,8 @@ __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const bool in = u * 64 + lane < nc;
-        pre[u] = in ? co_ld<CO>(row + u * 64 + lane) : 0;
-        pp[u] = in ? co_ld<CO>(prow + u * 64 + lane) : 0;
+        pre[u] = in ? row[u * 64 + lane] : 0;
+        pp[u] = in ? prow[u * 64 + lane] : 0;
     }
     int32_t carry = 0, below = 0;
     for (int c0 = 0; c0 < nc; c0 += 64) {
@@ -232,8 +204,8 @@ __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__
                 bq = c0 == u * 64 ? pp[u] : bq;
             }
         } else if (c < nc) {
-            v = co_ld<CO>(row + c);
-            bq = co_ld<CO>(prow + c);
+            v = row[c];
+            bq = prow[c];
         }
         int32_t incl = v;
 #pragma unroll
@@ -243,7 +215,7 @@ __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__
                 incl += u;
         }
         if (c < nc)
-            co_st<CO>(row + c, carry + incl - v);
+            row[c] = carry + incl - v;
         carry += __shfl(incl, 63, 64);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1)
@@ -251,7 +223,7 @@ __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__
         below += bq;
     }
     if (lane == 0) {
-        co_st<CO>(send_offset + e, below);
+        send_offset[e] = below;
         recv_count[e] = below + carry;
         tokens_per_expert[e] = carry;
     }
@@ -270,7 +242,6 @@ struct RankSrc {
 };
 
 // Resolves the K destination rows of token t: lane k < K holds row(t,k) or -1.
-template <bool CO>
 __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_idx,
                                              const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
                                              int T, int K, int E, int cap, int lane)
@@ -285,11 +256,10 @@ __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_id
                 dst = send_offset[e] + rs.send_token_idx[(size_t)t * K + lane];
         }
     } else if (lane < K) {
-        const int e = co_ld<CO>(topk_idx + (size_t)t * K + lane);
+        const int e = topk_idx[(size_t)t * K + lane];
         if (e >= 0 && e < E) {
             const int nc = (T + rs.tpc - 1) / rs.tpc;
-            dst = co_ld<CO>(send_offset + e) + co_ld<CO>(rs.chunk_base + (size_t)e * nc + t / rs.tpc) +
-                  co_ld<CO>(rs.chunk_rank + (size_t)t * K + lane);
+            dst = send_offset[e] + rs.chunk_base[(size_t)e * nc + t / rs.tpc] + rs.chunk_rank[(size_t)t * K + lane];
         }
     }
     if (dst >= cap)  // inconsistent counts: never write outside the output
@@ -304,7 +274,7 @@ __device__ __forceinline__ int dispatch_dest(const int32_t *__restrict__ topk_id
 // `ready()` is called between the loads of x and the first read of the routing results (a hook for a kernel
 // that waits there for earlier stages of the same launch; a no-op in the dispatch kernel).  skip_unrouted: a token none of whose
 // picks is below E reads nothing and only writes its row-map entries (`ready()` comes first then).
-template <int MODE, bool CO, typename Ready>
+template <int MODE, typename Ready>
 __device__ __forceinline__ void dispatch_wave(const uint16_t *__restrict__ x, const int32_t *__restrict__ topk_idx,
                                               const int32_t *__restrict__ send_offset, const RankSrc &rs, int t,
                                               int j, int T, int H, int K, int E, int rank, int cap,
@@ -321,7 +291,7 @@ __device__ __forceinline__ void dispatch_wave(const uint16_t *__restrict__ x, co
     if (skip_unrouted && topk_idx) {
         ready();
         waited = true;
-        const int e0 = lane < K ? co_ld<CO>(topk_idx + (size_t)t * K + lane) : -1;
+        const int e0 = lane < K ? topk_idx[(size_t)t * K + lane] : -1;
         if (__ballot(e0 >= 0 && e0 < E) == 0) {
             if (inv_out && j == 0 && lane < K)
                 inv_out[(size_t)t * K + lane] = -1;
@@ -342,7 +312,7 @@ __device__ __forceinline__ void dispatch_wave(const uint16_t *__restrict__ x, co
         }
         if (!waited)
             ready();
-        const int dst = dispatch_dest<CO>(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
         if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
             inv_out[(size_t)t * K + lane] = dst;
         for (int k = 0; k < K; ++k) {
@@ -375,7 +345,7 @@ __device__ __forceinline__ void dispatch_wave(const uint16_t *__restrict__ x, co
         }
         if (!waited)
             ready();
-        const int dst = dispatch_dest<CO>(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
+        const int dst = dispatch_dest(topk_idx, send_offset, rs, t, T, K, E, cap, lane);
         if (inv_out && j == 0 && lane < K)  // the combine's row map, so it needs no scatter pass
             inv_out[(size_t)t * K + lane] = dst;
         float f[16];

@@ -19,8 +19,8 @@ __global__ __launch_bounds__(ROUTE_WAVES * 64) void route_kernel(const float *__
                                                                  int32_t *__restrict__ chunk_pref = nullptr,
                                                                  int32_t *__restrict__ chunk_rank = nullptr)
 {
-    route_block<PER, HIST, false>(logits, bias, T, E, K, topk_idx, topk_w, topk_idx64, Ec, chunk_counts, chunk_pref,
-                                  chunk_rank, (int)blockIdx.x, (int)gridDim.x);
+    route_block<PER, HIST>(logits, bias, T, E, K, topk_idx, topk_w, topk_idx64, Ec, chunk_counts, chunk_pref,
+                           chunk_rank, (int)blockIdx.x, (int)gridDim.x);
 }
 
 hipError_t launch_route(const float *logits, const float *bias, int T, int E, int K, int32_t *topk_idx,
