@@ -156,10 +156,45 @@ def cpu_decode_baseline(x, logits, w1, s1, w2, s2, K, L, budget_s=10.0):
                       f"threads; {dt * 1e3:.1f} ms/step"}
 
 
+def cpu_layer_full(x, logits, bias, w1, s1, w2, s2, K, L, budget_s=8.0):
+    """The C oracle's whole fp8 layer on the layer's own inputs: route (with the expert bias) over all experts,
+    layout and count exchange over the L local experts, fp8 dispatch, GMM1 + SwiGLU + fp8 requant, GMM2,
+    combine; whole layers repeated until ~budget_s (at least one)."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    T = x.shape[0]
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    lg = logits.cpu().numpy()
+    bs = None if bias is None else bias.cpu().numpy()
+    u8 = lambda t: t.cpu().contiguous().view(torch.uint8).numpy()  # noqa: E731
+    hw1, hw2, hs1, hs2 = u8(w1), u8(w2), s1.cpu().numpy(), s2.cpu().numpy()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        idx, w = orc.route(lg, bs, K)
+        rid = np.where(idx < L, idx, -1).astype(np.int32)
+        _, nte, _, sti = orc.dispatch_layout(rid.astype(np.int64), L, 1)
+        so, _, _, _ = orc.notify_dispatch(nte)
+        ex, xs, eidx = orc.dispatch(xb, rid, so, sti, L, orc.QUANT_FP8)
+        cnt = nte.astype(np.int64)
+        hq, hs = orc.gmm1_swiglu_fp8(ex, xs, cnt, hw1, hs1)
+        y = orc.gmm2_fp8(hq, hs, cnt, hw2, hs2)
+        orc.combine(y, eidx, rid, w, L)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    threads = orc.num_threads()
+    return {"value": T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} whole layer(s) on the same inputs through the C oracle (route with the expert bias, "
+                      f"layout, fp8 dispatch, GMM1+SwiGLU, GMM2, combine; {int(cnt.sum())} local rows), {threads} "
+                      f"OpenMP threads; {dt:.2f} s per layer"}
+
+
 def cpu_layer_baseline(cfg_cpu, dt, T, H, I, M, seed):
-    """CPU oracle time of one layer: route + layout + dispatch + combine at the config-2 shapes (the same
-    T, H, E, K as config 4; cfg_cpu is that measured step, None for config 3, whose bookkeeping is
-    < 1% of its GEMMs) + M rows of the oracle's expert GEMMs."""
+    """CPU oracle time of one layer too long to run whole (config 3: ~80 s per layer): a ~5 s sample of rows
+    through the oracle's expert GEMMs scaled to M, plus cfg_cpu's measured bookkeeping step when given (None
+    for config 3, whose bookkeeping is < 1% of its GEMMs)."""
     from oracle import oracle as orc
     per_row, n = cpu_gemm_row_seconds(dt, H, I, seed)
     step = (T / cfg_cpu["value"]) if cfg_cpu else 0.0
@@ -278,8 +313,9 @@ def make_weights(L, H, I, dtype, dev, seed):
     return w1, s1, w2, s2
 
 
-def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
-    """Full layer (route, layout, dispatch, GMM1+SwiGLU, GMM2, combine) on one rank's L local experts."""
+def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind, cpu=False):
+    """Full layer (route, layout, dispatch, GMM1+SwiGLU, GMM2, combine) on one rank's L local experts.  cpu
+    (fp8 only): also time the C oracle's whole layer on the same inputs (cpu_layer_full)."""
     from umdk_amd.plan import MoeLayerPlan
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(seed)
@@ -313,13 +349,17 @@ def run_layer(name, T, H, E, K, L, I, dtype, steps, warmup, seed, bias_kind):
     ab2 = M * I * esz + M * H * 2 + wb2
     roof = max(f1 / (peak * 1e12), ab1 / (HBM_PEAK_GBPS * 1e9)) + max(f2 / (peak * 1e12), ab2 / (HBM_PEAK_GBPS * 1e9))
     tflops = (f1 + f2) / (gx * 1e-3) / 1e12
+    cpu_res = cpu_layer_full(x, logits, bias, w1, s1, w2, s2, K, L) if cpu and dtype == "fp8" else None
     del w1, w2
-    return {"workload": name, "tokens": T, "hidden": H, "experts_routed": E, "local_experts": L, "topk": K,
+    res = {"workload": name, "tokens": T, "hidden": H, "experts_routed": E, "local_experts": L, "topk": K,
             "intermediate": I, "dtype": dtype, "local_rows_M": M, "experts_touched": touched,
             "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
             "experts_ms": gx, "gmm1_ms": g1, "gmm2_ms": g2, "gemm_tflops": tflops,
             "gemm_frac_of_mfma_peak": tflops / peak, "gemm_roofline_frac": roof / (gx * 1e-3),
             "gemm_bound": "mfma" if (f1 + f2) / (peak * 1e12) > (ab1 + ab2) / (HBM_PEAK_GBPS * 1e9) else "hbm"}
+    if cpu_res:
+        res["cpu_baseline"] = cpu_res
+    return res
 
 
 def measured_peaks():
@@ -523,14 +563,14 @@ def main():
 
     cfg3 = lambda st, wu: run_layer("config3: Mixtral-8x7B grouped SwiGLU FFN, bf16", 8192, 4096, 8, 2, 8, 14336,
                                     "bf16", st, wu, args.seed, None)
-    cfg4 = lambda st, wu, dt="fp8": run_layer(
+    cfg4 = lambda st, wu, dt="fp8", cpu=False: run_layer(
         f"config4: DeepSeek-V3 one-rank layer (32 of 256 experts, Zipf 1.1), {dt}", 4096, 7168, 256, 8, 32, 2048,
-        dt, st, wu, args.seed, "zipf")
+        dt, st, wu, args.seed, "zipf", cpu)
     if args.config == "peaks":
         print(json.dumps({"config": "peaks", "result": measured_peaks()}))
         return
     if args.config in ("3", "4", "4i8", "5", "5i8", "sweep", "sweepi8"):
-        r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup),
+        r = {"3": lambda: cfg3(args.steps, args.warmup), "4": lambda: cfg4(args.steps, args.warmup, cpu=not args.no_cpu),
              "4i8": lambda: cfg4(args.steps, args.warmup, "int8"),
              "5": lambda: run_decode(max(args.steps, 1000), args.seed, cpu=not args.no_cpu),
              "5i8": lambda: run_decode(max(args.steps, 1000), args.seed, "int8"),
@@ -634,7 +674,7 @@ def main():
         torch.cuda.empty_cache()
         result["config3"] = cfg3(10, 3)
         torch.cuda.empty_cache()
-        result["config4"] = cfg4(20, 5)
+        result["config4"] = cfg4(20, 5, cpu=not args.no_cpu)
         result["config4_int8"] = cfg4(20, 5, "int8")
         torch.cuda.empty_cache()
     if args.config in ("default", "all"):
@@ -645,9 +685,6 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(T, H, E, K, args.seed)
         if args.config in ("default", "all"):
-            c4 = result["config4"]
-            c4["cpu_baseline"] = cpu_layer_baseline(result["cpu_baseline"], "fp8", 4096, 7168, 2048,
-                                                    c4["local_rows_M"], args.seed)
             c3 = result["config3"]
             c3["cpu_baseline"] = cpu_layer_baseline(None, "bf16", 8192, 4096, 14336, c3["local_rows_M"], args.seed)
     print(json.dumps(result))
