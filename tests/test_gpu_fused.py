@@ -285,3 +285,34 @@ def test_fused_rejects_unsupported(ops):
         sm = torch.ones(8, 1024, device="cuda")
         ops.fused_deep_moe(d["x"], d["ids"], [d["w1"].transpose(1, 2)], [], [d["w2"].transpose(1, 2)], [],
                            d["scales"], None, None, None, None, sm, None, None, "ep", 1, 0, 8, 0, 0)
+
+
+def test_fused_decode_fresh_inputs_and_forced_give_up(ops):
+    """The decode path (layout and dispatch in one launch, then the chained GEMMs, whose GMM2 tiles read h
+    written by other blocks of the same launch): consecutive calls on new activations and ids each time equal
+    the small-op chain (a row of the previous call read from a stale cache would show); then, with every
+    readiness wait made unreachable from the host and a 20 us bound, the call ends normally and reports through
+    the sync status, and the next call is exact again."""
+    from umdk_amd import _lib
+    bs, H, I, E, K = 128, 2048, 256, 32, 8
+    for seed in range(3):
+        print(f"fused decode, fresh inputs: seed {seed}", flush=True)
+        d = make(40 + seed, bs, H, I, E, K, "fp8")
+        out, _, etn = call_fused(ops, d, E)
+        ref, rtpe = chain_small_ops(ops, d, E, K)
+        assert torch.equal(etn, rtpe)
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    print("fused decode, forced give-up", flush=True)
+    torch.cuda.synchronize()
+    _lib.sync_status(clear=True)
+    L = _lib.lib()
+    L.camhipDebugSetSyncWait(2000, 1)
+    try:
+        call_fused(ops, d, E)
+        torch.cuda.synchronize()
+    finally:
+        L.camhipDebugSetSyncWait(0, 0)
+    assert _lib.sync_status(clear=True) != 0, "an unreachable wait did not report"
+    out, _, etn = call_fused(ops, d, E)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)) and torch.equal(etn, rtpe)
+    assert _lib.sync_status() == 0

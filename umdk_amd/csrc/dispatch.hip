@@ -170,8 +170,8 @@ __global__ __launch_bounds__(DISP_WAVES * 64) void dispatch_int8_kernel(
 // chained GEMMs' counters).
 constexpr int DEC_WAVES = 16;
 constexpr int DEC_THREADS = DEC_WAVES * 64;
-constexpr int DEC_MAX_TK = 2048;
-constexpr int DEC_MAX_E = 512;
+constexpr int DEC_MAX_TK = LAYOUT_LDS_MAX_TK;
+constexpr int DEC_MAX_E = LAYOUT_LDS_MAX_E;
 
 template <int MODE>
 __global__ __launch_bounds__(DEC_THREADS) void dispatch_decode_kernel(
@@ -181,97 +181,22 @@ __global__ __launch_bounds__(DEC_THREADS) void dispatch_decode_kernel(
     int32_t *__restrict__ send_offset, int32_t *__restrict__ recv_count, int32_t *__restrict__ total,
     int64_t *__restrict__ tokens_per_expert, int32_t *__restrict__ zero, int nzero)
 {
-    __shared__ int32_t s_ids[DEC_MAX_TK], s_rank[DEC_MAX_TK];
-    __shared__ int32_t s_run[DEC_MAX_E], s_off[DEC_MAX_E];
-    __shared__ int32_t s_wh[DEC_WAVES][DEC_MAX_E];
-    __shared__ int32_t s_wsum[DEC_WAVES];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    for (long i = (long)blockIdx.x * DEC_THREADS + tid; i < nzero; i += (long)gridDim.x * DEC_THREADS)
+    __shared__ LayoutLds<DEC_THREADS> s;
+    for (long i = (long)blockIdx.x * DEC_THREADS + threadIdx.x; i < nzero; i += (long)gridDim.x * DEC_THREADS)
         zero[i] = 0;
-    const int TK = T * K;
     auto layout = [&]() {
-        for (int e = tid; e < E; e += DEC_THREADS)
-            s_run[e] = 0;
-        const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
-        const uint64_t lt = lanemask_lt();
-        for (int base = 0; base < TK; base += DEC_THREADS) {
-            for (int j = tid; j < DEC_WAVES * E; j += DEC_THREADS)
-                s_wh[j / E][j % E] = 0;
-            __syncthreads();
-            const int i = base + tid;
-            int e = -1;
-            if (i < TK) {
-                const int id = ids[i];
-                e = (active == nullptr || active[i / K] != 0) && id >= 0 && id < E ? id : -1;
-                s_ids[i] = e;
-            }
-            const bool valid = e >= 0;
-            uint64_t peers = __ballot(valid);
-            for (int b = 0; b < nbits; ++b) {
-                const bool bit = valid && ((e >> b) & 1);
-                const uint64_t m = __ballot(bit);
-                peers &= bit ? m : ~m;
-            }
-            const int inrank = __popcll(peers & lt);
-            if (valid && inrank == 0)
-                s_wh[w][e] = __popcll(peers);
-            __syncthreads();
-            if (i < TK) {
-                int32_t r = -1;
-                if (valid) {
-                    r = s_run[e] + inrank;
-                    for (int ww = 0; ww < w; ++ww)
-                        r += s_wh[ww][e];
-                }
-                s_rank[i] = r;
-            }
-            __syncthreads();
-            for (int ee = tid; ee < E; ee += DEC_THREADS) {
-                int32_t acc = 0;
-#pragma unroll
-                for (int ww = 0; ww < DEC_WAVES; ++ww)
-                    acc += s_wh[ww][ee];
-                s_run[ee] += acc;
-            }
-            __syncthreads();
-        }
-        // count exchange of one rank: thread e owns expert e (E <= DEC_THREADS)
-        const int c = tid < E ? s_run[tid] : 0;
-        int32_t v = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int32_t u = __shfl_up(v, o, 64);
-            if (lane >= o)
-                v += u;
-        }
-        if (lane == 63)
-            s_wsum[w] = v;
-        __syncthreads();
-        int32_t before = 0;
-        for (int ww = 0; ww < w; ++ww)
-            before += s_wsum[ww];
-        const int32_t incl = before + v;
-        if (tid < E) {
-            s_off[tid] = incl - c;
-            if (blockIdx.x == 0) {
-                counts[tid] = c;
-                send_offset[tid] = incl - c;
-                recv_count[tid] = incl;
-                tokens_per_expert[tid] = c;
-                if (tid == E - 1)
-                    *total = incl;
-            }
-        }
-        __syncthreads();
+        layout_lds<DEC_THREADS>(ids, active, T, K, E, s);
+        if (blockIdx.x == 0)
+            layout_lds_store(s, E, counts, send_offset, recv_count, total, tokens_per_expert);
     };
-    const long item = (long)blockIdx.x * DEC_WAVES + w;
+    const long item = (long)blockIdx.x * DEC_WAVES + (threadIdx.x >> 6);
     if (item >= (long)T * nchunk) {  // a wave without an item still takes its part in the block's layout
         layout();
         return;
     }
     const int t = (int)(item / nchunk), j = (int)(item % nchunk);
-    const RankSrc rs{s_rank, nullptr, nullptr, 0};
-    dispatch_wave<MODE>(x, s_ids, s_off, rs, t, j, T, H, K, E, 0, cap, expand_x, scales, expand_idx, inv_out,
+    const RankSrc rs{s.rank, nullptr, nullptr, 0};
+    dispatch_wave<MODE>(x, s.ids, s.off, rs, t, j, T, H, K, E, 0, cap, expand_x, scales, expand_idx, inv_out,
                         kmajor, 0, layout);
 }
 

@@ -229,6 +229,136 @@ __device__ __forceinline__ void scan_expert(int e, int nc, int32_t *__restrict__
     }
 }
 
+// ---------------------------------------------------------------- D1 + D2 of a decode step, in one block
+// The whole layout of T*K <= LAYOUT_LDS_MAX_TK picks over E <= LAYOUT_LDS_MAX_E experts, computed by one block
+// of NT threads into LDS: the effective id of every pick (-1 when masked or outside [0, E)), its stable rank
+// among the picks of its expert in (t,k) order (lanes sharing an expert found with one ballot per bit of the
+// id, waves ordered by per-wave counts, windows of NT picks in turn), the count of every expert and its
+// exclusive offset (the count exchange of one rank).  The same results as layout_small_kernel.
+constexpr int LAYOUT_LDS_MAX_TK = 2048;
+constexpr int LAYOUT_LDS_MAX_E = 512;
+template <int NT> struct LayoutLds {
+    int32_t ids[LAYOUT_LDS_MAX_TK], rank[LAYOUT_LDS_MAX_TK];
+    int32_t count[LAYOUT_LDS_MAX_E], off[LAYOUT_LDS_MAX_E];
+    int32_t wave_hist[NT / 64][LAYOUT_LDS_MAX_E];
+    int32_t wave_sum[NT / 64];
+};
+template <int NT>
+__device__ __forceinline__ void layout_lds(const int32_t *__restrict__ ids, const uint8_t *__restrict__ active, int T,
+                                           int K, int E, LayoutLds<NT> &s)
+{
+    constexpr int NW = NT / 64, NPASS = LAYOUT_LDS_MAX_TK / NT, PE = (LAYOUT_LDS_MAX_E + NT - 1) / NT;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, TK = T * K;
+    // every pick's effective id first: unconditional loads (indices clamped to the last pick), all in flight
+    // together
+    int eff[NPASS], on[NPASS];
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+        eff[q] = ids[min(q * NT + tid, TK - 1)];
+        on[q] = 1;
+    }
+    if (active) {
+#pragma unroll
+        for (int q = 0; q < NPASS; ++q)
+            on[q] = active[min(q * NT + tid, TK - 1) / K];
+    }
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+        const int id = eff[q];
+        eff[q] = q * NT + tid < TK && on[q] != 0 && id >= 0 && id < E ? id : -1;
+    }
+    for (int e = tid; e < E; e += NT)
+        s.count[e] = 0;
+    const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+    const uint64_t lt = lanemask_lt();
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+        if (q * NT >= TK)
+            break;
+        for (int j = tid; j < NW * E; j += NT)
+            s.wave_hist[j / E][j % E] = 0;
+        __syncthreads();
+        const int i = q * NT + tid, e = eff[q];
+        if (i < TK)
+            s.ids[i] = e;
+        const bool valid = e >= 0;
+        uint64_t peers = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const int inrank = __popcll(peers & lt);
+        if (valid && inrank == 0)
+            s.wave_hist[w][e] = __popcll(peers);
+        __syncthreads();
+        if (i < TK) {
+            int32_t r = -1;
+            if (valid) {
+                r = s.count[e] + inrank;
+                for (int ww = 0; ww < w; ++ww)
+                    r += s.wave_hist[ww][e];
+            }
+            s.rank[i] = r;
+        }
+        __syncthreads();
+        for (int ee = tid; ee < E; ee += NT) {
+            int32_t acc = 0;
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww)
+                acc += s.wave_hist[ww][ee];
+            s.count[ee] += acc;
+        }
+        __syncthreads();
+    }
+    // exclusive offsets over the experts: thread i owns experts [i PE, (i + 1) PE)
+    int cnt[PE], own = 0;
+#pragma unroll
+    for (int u = 0; u < PE; ++u) {
+        const int e = tid * PE + u;
+        cnt[u] = e < E ? s.count[e] : 0;
+        own += cnt[u];
+    }
+    int32_t v = own;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int32_t u = __shfl_up(v, o, 64);
+        if (lane >= o)
+            v += u;
+    }
+    if (lane == 63)
+        s.wave_sum[w] = v;
+    __syncthreads();
+    int32_t run = v - own;
+    for (int ww = 0; ww < w; ++ww)
+        run += s.wave_sum[ww];
+#pragma unroll
+    for (int u = 0; u < PE; ++u) {
+        const int e = tid * PE + u;
+        if (e < E)
+            s.off[e] = run;
+        run += cnt[u];
+    }
+    __syncthreads();
+}
+// The layout's global outputs (by one block): counts, send offsets, inclusive counts, the total and the int64
+// tokens per expert.
+template <int NT>
+__device__ __forceinline__ void layout_lds_store(const LayoutLds<NT> &s, int E, int32_t *__restrict__ counts,
+                                                 int32_t *__restrict__ send_offset, int32_t *__restrict__ recv_count,
+                                                 int32_t *__restrict__ total, int64_t *__restrict__ tokens_per_expert)
+{
+    for (int e = threadIdx.x; e < E; e += NT) {
+        const int32_t c = s.count[e], o = s.off[e];
+        counts[e] = c;
+        send_offset[e] = o;
+        recv_count[e] = o + c;
+        tokens_per_expert[e] = c;
+        if (e == E - 1)
+            *total = o + c;
+    }
+}
+
 // ---------------------------------------------------------------- D3 + Q1: one dispatch wave
 // Where the rank of (t,k) within its expert comes from: send_token_idx[t,k] (the layout op's output), or,
 // with send_token_idx == nullptr, chunk_base (the prefill step: chunks of `tpc` tokens, chunk_base[e * nc + c]
