@@ -59,6 +59,12 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 #ifndef CAM_GMM_MIN_NK256
 #define CAM_GMM_MIN_NK256 16
 #endif
+#ifndef CAM_GMM_UNROLL2
+// the 256-row tile's k-loop unrolled by two, so that the ring slot of each step is a constant and every LDS
+// address an immediate offset (measured: the M = 65536 fp8 GMM1 2.18 vs 2.13 PFLOPS, config 3's bf16 GEMMs
+// 1.31 vs 1.27 PFLOPS, config 4's 278-284 vs 286 us; fewer address and scalar instructions per k-step)
+#define CAM_GMM_UNROLL2 1
+#endif
 #ifndef CAM_GMM_NT_MAXBM
 #define CAM_GMM_NT_MAXBM 32  // tile heights up to this stream their weights nontemporally
 #endif
@@ -875,13 +881,17 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                 pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
                 ps[j] = 0.0f;
             }
-            auto kloop = [&](auto act) {
-                for (int ks = 0; ks < nk; ++ks) {
+            // one k-step; SL = ks & 1, the ring slot (a compile-time constant under CAM_GMM_UNROLL2, so that
+            // every LDS address of the step is an immediate offset)
+            auto kstep = [&](auto act, int ks, auto slc) {
+                {
+                    constexpr int SL0 = decltype(slc)::value;
+                    const int SL = SL0 >= 0 ? SL0 : (ks & 1);
                     // k-step ks has landed (only the W bands of ks+1, issued last, may still be in flight);
                     // this wave's reads of k-step ks-1 are done
                     wait_vmcnt_lgkm0<B_LOADS>();
                     bar();  // ... for every wave: the A/scale slot (ks+1)%2 is free
-                    const uint8_t *st = smem + (ks & 1) * STAGE_BYTES;
+                    const uint8_t *st = smem + SL * STAGE_BYTES;
                     const uint8_t *la = st + (wm * WM) * GKB;
                     const uint8_t *lb = st + A_BYTES + (wn * WN) * GKB;
                     i32x8 b[JF], a[IF];
@@ -954,13 +964,13 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                             if (n < HALF) {
 #pragma unroll
                                 for (int u = n * AS / HALF; u < (n + 1) * AS / HALF; ++u)
-                                    dma_one(c, kn, (ks + 1) & 1, u < A_LOADS ? u : u + B_LOADS);
+                                    dma_one(c, kn, 1 - SL, u < A_LOADS ? u : u + B_LOADS);
                             }
                             if (n == HALF) {
                                 bar();
 #pragma unroll
                                 for (int q = A_LOADS; q < A_LOADS + B_LOADS; ++q)
-                                    dma_one(c, min(ks + 2, nk - 1), ks & 1, q);
+                                    dma_one(c, min(ks + 2, nk - 1), SL, q);
                             }
                             if constexpr (FP8) {
                                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -972,6 +982,20 @@ __device__ __forceinline__ void gmm_body(const GmmArgs &p, const GroupTables *gt
                         }
                     }
                 }
+            };
+            auto kloop = [&](auto act) {
+#if CAM_GMM_UNROLL2
+                int ks = 0;
+                for (; ks + 1 < nk; ks += 2) {
+                    kstep(act, ks, std::integral_constant<int, 0>{});
+                    kstep(act, ks + 1, std::integral_constant<int, 1>{});
+                }
+                if (ks < nk)
+                    kstep(act, ks, std::integral_constant<int, 0>{});
+#else
+                for (int ks = 0; ks < nk; ++ks)
+                    kstep(act, ks, std::integral_constant<int, -1>{});
+#endif
             };
             if (c.active)
                 kloop(std::true_type{});
